@@ -1,0 +1,53 @@
+"""MXFP4 dequant (bit-exact) and the weight-only linear (single MXFP4 linear workload:
+W [5760 x 2880], x [128 x 2880]) against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4 as om
+
+pytestmark = pytest.mark.gpu
+
+
+def test_dequant_every_scale_and_code_bit_exact(dev):
+    from vllm_neuron_amd.functional import dequantize_mxfp4_to_bf16
+
+    codes = np.arange(32) % 16
+    byte = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)
+    blocks = torch.from_numpy(np.tile(byte, (256, 1))).reshape(256, 1, 16)
+    scales = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(256, 1)
+    want = om.dequantize_mxfp4_to_bf16(blocks, scales).view(torch.int16)
+    got = dequantize_mxfp4_to_bf16(blocks.to(dev), scales.to(dev)).cpu().view(torch.int16)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows,K", [(5760, 2880), (7, 32), (3, 2048)])
+def test_dequant_random_bit_exact(dev, rows, K):
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.functional import dequantize_mxfp4_to_bf16
+
+    blocks, scales = synthetic.mxfp4_tensor(rows + K, rows, K, 0, 255)
+    want = om.dequantize_mxfp4_to_bf16(blocks, scales).view(torch.int16)
+    got = dequantize_mxfp4_to_bf16(blocks.to(dev), scales.to(dev)).cpu().view(torch.int16)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 5760, 2880), (1, 16, 32), (37, 48, 96), (300, 64, 2048)])
+def test_linear(dev, M, N, K):
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.functional import mxfp4_linear
+    from vllm_neuron_amd.weights import pack_mxfp4
+
+    blocks, scales = synthetic.mxfp4_tensor(11 + N, N, K)
+    x = synthetic.normal_bf16(12 + M, (M, K))
+    want = om.mxfp4_linear(x, blocks, scales).float()
+    wq, ws = pack_mxfp4(blocks, scales)
+    got = mxfp4_linear(x.to(dev), wq.to(dev), ws.to(dev)).float().cpu()
+    d = (got - want).abs()
+    # same bf16 products, different fp32 summation order: at most one bf16 ulp apart
+    ulp = torch.maximum(want.abs(), got.abs()) * 2.0 ** -7
+    assert torch.all(d <= ulp + 1e-30), d.max()
+    frac_exact = (d == 0).float().mean().item()
+    print(f"linear {M}x{N}x{K}: bit-identical fraction {frac_exact:.4f}")
+    assert frac_exact > 0.9

@@ -1,0 +1,136 @@
+"""Decode expert path (router -> moe_tkg) vs the oracle's moe_block_tkg flow (fp32)."""
+
+import pytest
+import torch
+
+from moe_helpers import build, check_close, routing_agreement
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gptoss20(dev):
+    from vllm_neuron_amd import synthetic
+
+    return build(synthetic.GPT_OSS_20B, 1, dev)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64])
+def test_decode_gptoss20b(dev, gptoss20, T):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = gptoss20
+    x = synthetic.tokens(21, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.decode(x.to(dev)).cpu()
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, f"decode 20b T={T}")
+
+
+def test_decode_unsaturated_weights(dev):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 2, dev, E=16, exp=(116, 120))
+    x = synthetic.tokens(22, 40, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.decode(x.to(dev)).cpu()
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, "decode unsaturated")
+
+
+def test_decode_dense_flow_equals_routed(dev):
+    """The dense all-expert flow of the reference on a small layer, end to end."""
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 512)
+    ref, layer, _ = build(shape, 3, dev, exp=(118, 122))
+    x = synthetic.tokens(23, 9, ref.H)
+    want, aff = ref.decode(x)
+    got = layer.decode(x.to(dev)).cpu()
+    check_close(got, want, None, "decode dense mini")
+
+
+def test_decode_plain_swiglu_fine_grained(dev):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.FINE_GRAINED, 4, dev, E=32)
+    x = synthetic.tokens(24, 8, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.decode(x.to(dev)).cpu()
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, "decode plain swiglu")
+
+
+def test_moe_tkg_api_ep_rank_and_no_scale(dev):
+    """moe_tkg with global expert ids and rank_id (local slice), NO_SCALE mode."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import moe_block_tkg as obt
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 5, dev, exp=(118, 122))
+    T, E_g = 12, 16
+    x = synthetic.tokens(25, T, ref.H)
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(T, E_g, generator=g)
+    vals, idx = torch.topk(logits, 2, dim=1)
+    aff_full = torch.zeros(T, E_g).scatter_(1, idx, torch.softmax(vals, 1))
+    w = layer.w
+    got = NF.moe_tkg(x.to(dev), w.gu_q, w.dn_q, aff_full.to(dev), idx.to(torch.int32).to(dev),
+                     is_all_expert=False, rank_id=torch.tensor([[1]], device=dev),
+                     expert_gate_up_bias=w.gu_bias, expert_down_bias=w.dn_bias,
+                     expert_gate_up_weights_scale=w.gu_s, expert_down_weights_scale=w.dn_s,
+                     expert_affinities_scaling_mode="NO_SCALE", activation_fn="Swish",
+                     gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                     up_clamp_lower_limit=-6.0).cpu()
+    local = aff_full[:, 8:16]
+    gu = ref.gate_up.reshape(8, ref.H, 2, ref.I)
+    want = obt.expert_mlp_fp32_routed(x, local, gu, ref.down, ref.gu_bias.reshape(8, 2, ref.I),
+                                      ref.dn_bias, hidden_act_fn="Swish",
+                                      gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                                      up_clamp_lower_limit=-6.0, scale_mode="NO_SCALE",
+                                      out_dtype=torch.bfloat16)
+    rows = (local != 0).any(1)
+    assert torch.all(got[~rows] == 0)
+    check_close(got[rows], want[rows], None, "moe_tkg ep rank 1, NO_SCALE")
+
+
+def test_moe_block_tkg_api(dev):
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import moe_block_tkg as obt
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 6, dev, E=32)
+    T = 16
+    x = synthetic.tokens(26, T, ref.H)
+    gamma = torch.ones(ref.H)
+    w = layer.w
+    out, logits = NF.moe_block_tkg(
+        x.unsqueeze(0).to(dev), gamma.unsqueeze(0).to(dev), ref.router_w.T.to(dev), w.gu_q, w.dn_q,
+        top_k=4, expert_gate_up_weights_scale=w.gu_s, expert_down_weights_scale=w.dn_s,
+        expert_gate_up_bias=w.gu_bias, expert_down_bias=w.dn_bias, router_act_fn="SOFTMAX",
+        router_pre_norm=False, expert_affinities_scaling_mode="POST_SCALE",
+        hidden_act_fn="Swish", gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+        up_clamp_lower_limit=-6.0)
+    xn, logits_r, top, idx = obt.rmsnorm_router(x, gamma, ref.router_w.T, None, 1e-6, 4,
+                                                "SOFTMAX", False, False)
+    aff = torch.zeros(T, ref.E).scatter_(1, idx, top)
+    want = ref.decode_routed(xn, aff)
+    assert torch.allclose(logits.cpu(), logits_r, rtol=1e-5, atol=1e-5)
+    check_close(out.cpu(), want, None, "moe_block_tkg")
+
+
+def test_decode_gptoss120b_t64_sample(dev):
+    """120B-shaped layer (128 experts) at 64 tokens: a sample of 8 tokens against the
+    oracle (per-token outputs depend only on the token's own row and routing)."""
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.GPT_OSS_120B, 7, dev)
+    x = synthetic.tokens(27, 64, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.decode(x.to(dev)).cpu()
+    rows = torch.arange(0, 64, 8)
+    want = ref.decode_routed(x[rows], aff[rows])
+    check_close(got[rows], want, ties[rows], "decode 120b T=64 sample")

@@ -1,0 +1,91 @@
+"""Prefill expert path (router -> blockwise mapping -> moe_cte) vs the oracle's
+moe_cte torch flow (bf16 intermediates)."""
+
+import pytest
+import torch
+
+from moe_helpers import build, check_close, routing_agreement
+
+pytestmark = pytest.mark.gpu
+
+
+def test_prefill_dense_flow_mini(dev):
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 512)
+    ref, layer, _ = build(shape, 31, dev, exp=(118, 122))
+    x = synthetic.tokens(31, 300, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    want, _ = ref.prefill(x, aff)
+    got = layer.prefill(x.to(dev)).cpu()
+    check_close(got, want, ties, "prefill dense mini")
+
+
+@pytest.mark.parametrize("T,zipf", [(512, None), (4096, None), (4096, 1.2)])
+def test_prefill_gptoss20b(dev, T, zipf):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 32 if zipf is None else 33, dev, zipf=zipf)
+    x = synthetic.tokens(32, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev)).cpu()
+    rows = torch.arange(0, T, max(1, T // 48))
+    want = ref.prefill_routed(x, aff, token_rows=rows)
+    check_close(got[rows], want, ties[rows], f"prefill 20b T={T} zipf={zipf}")
+
+
+def test_prefill_unsaturated(dev):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 34, dev, E=16, exp=(116, 120))
+    x = synthetic.tokens(34, 700, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev)).cpu()
+    rows = torch.arange(0, 700, 7)
+    want = ref.prefill_routed(x, aff, token_rows=rows)
+    check_close(got[rows], want, ties[rows], "prefill unsaturated")
+
+
+def test_prefill_plain_swiglu_fine_grained(dev):
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.FINE_GRAINED, 35, dev, E=32, zipf=1.0)
+    x = synthetic.tokens(35, 512, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev)).cpu()
+    rows = torch.arange(0, 512, 16)
+    want = ref.prefill_routed(x, aff, token_rows=rows)
+    check_close(got[rows], want, ties[rows], "prefill plain swiglu")
+
+
+def test_moe_cte_api_padding_and_skip_token(dev):
+    """moe_cte through the reference call pattern with a padding mask; padded tokens
+    keep their slots but contribute with zero affinity."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 36, dev, exp=(118, 122))
+    T = 200
+    x = synthetic.tokens(36, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    assert not ties.any()
+    pm = torch.arange(T) < 150
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), 8, 2, 256, padding_mask=pm.to(dev))
+    w = layer.w
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, b2e, 256, conditions=cond,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function="Swish", skip_token=True,
+                     expert_affinities_scaling_mode="POST_SCALE", gate_clamp_upper_limit=7.0,
+                     up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, 8, 2, 256, padding_mask=pm)
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, am_r, gu, ref.down, gb, db, gate_clamp_upper_limit=7.0,
+                             up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0,
+                             activation_function="Swish")
+    assert torch.all(got[150:] == 0)
+    check_close(got[:150], want[:150], None, "moe_cte padding mask")

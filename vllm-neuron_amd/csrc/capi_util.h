@@ -1,0 +1,48 @@
+// Host-side helpers shared by the C-ABI entry points: per-thread error text,
+// argument checks, HIP status propagation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/mxfp4_moe.h"
+
+namespace mxmoe {
+
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Status of the launches just issued on the stream (does not synchronize).
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MXMOE_E_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MXMOE_OK;
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over a caller-provided workspace.
+struct Carver {
+  char* base;
+  size_t cap;
+  size_t off = 0;
+  Carver(void* b, size_t c) : base(static_cast<char*>(b)), cap(c) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    T* p = reinterpret_cast<T*>(base + off);
+    off += count * sizeof(T);
+    return p;
+  }
+  bool ok() const { return off <= cap; }
+};
+
+}  // namespace mxmoe
+
+#define MXMOE_REQUIRE(cond, ...)                                    \
+  do {                                                              \
+    if (!(cond)) return ::mxmoe::set_error(MXMOE_E_INVALID, __VA_ARGS__); \
+  } while (0)

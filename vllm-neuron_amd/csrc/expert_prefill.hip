@@ -1,0 +1,431 @@
+// Prefill (context encoding) expert MLP over the blockwise mapping.
+//
+// Both projections run the same LDS-tiled grouped GEMM:
+//   workgroup tile = 128 slots (M) x 256 weight rows (N, 16 row groups) x 128-wide
+//   K chunks, 8 waves as 2 (M) x 4 (N), each wave 64 slots x 64 rows = 4 x 4
+//   MFMA 16x16x32 tiles.  A chunk of activations (128 x 128 bf16, rows padded to
+//   272 bytes against bank conflicts) and of packed weights (16 x 1 KiB + 16 x 64
+//   scale bytes) is staged per step, double-buffered with one barrier per step;
+//   the next chunk's global loads are in flight while the current one computes.
+//   Weights are dequantized from LDS to bf16 in registers by the CDNA4 scaled
+//   conversion, right before the MFMAs.
+//   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one
+//   expert; tiles whose 128 slots are all padding exit at once.  Tiles are
+//   ordered N-fastest and dealt out XCD by XCD, so the workgroups sharing an
+//   M-tile's activations (and an expert's weights) sit on the same L2.
+// gate_up: A = x rows gathered through token_position_to_id; epilogue = bias,
+//          clamps, activation and up * act with the reference's bf16 roundings;
+//          writes h [slots, I] bf16.
+// down:    A = h rows of the same slots; epilogue = bias with bf16 roundings;
+//          writes y [slots, H] bf16.
+// combine: out[t] = bf16(sum over experts in ascending id of y * affinity) in fp32.
+#include <math.h>
+
+#include "capi_util.h"
+#include "common.h"
+
+namespace mxmoe {
+
+constexpr int kPM = 128;    // slots per M-tile
+constexpr int kPRG = 16;    // row groups per N-tile (256 rows)
+constexpr int kARow = 272;  // LDS bytes per activation row of a chunk (256 + 16 pad)
+constexpr int kPThreads = 512;
+
+struct PrefillArgs {
+  const uint16_t* a;      // x [T, H] (gate_up) or h [slots, I] (down)
+  const uint8_t* wq;      // packed weights, all experts
+  const uint8_t* ws;      // packed scales
+  const uint16_t* bias;   // gate_up: [E, 2, I]; down: [E, H]; may be null
+  const int32_t* tp2id;   // token_position_to_id [slots]
+  const int32_t* b2e;     // block_to_expert [n_blocks]
+  uint16_t* out;          // h [slots, I] or y [slots, H]
+  int T, K, N_rows, I, H, B;
+  int n_mtiles, n_ntiles;
+  ExpertParams p;
+};
+
+__device__ __forceinline__ float rb(float v) { return round_bf16(v); }
+
+__device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
+  v = (v > hi) ? hi : v;
+  v = (v < lo) ? lo : v;
+  return v;
+}
+
+// Activation on a bf16 value with the reference's bf16 intermediate roundings.
+__device__ __forceinline__ float act_bf16(float g, int act) {
+  if (act == kSwish) {
+    const float t1 = rb(g * 1.702f);
+    const float t2 = rb(1.0f / (1.0f + expf(-t1)));
+    return rb(g * t2);
+  }
+  if (act == kSiLU) return rb(g / (1.0f + expf(-g)));
+  return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
+}
+
+template <bool GATE_UP>
+__global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t sa[2][kPM * kARow];
+  __shared__ __attribute__((aligned(16))) uint8_t sb[2][kPRG * 1024];
+  __shared__ __attribute__((aligned(16))) uint8_t ss[2][kPRG * 64];
+  __shared__ int32_t stok[kPM];
+  __shared__ int s_any;
+
+  // XCD-aware tile order (workgroups are dealt round-robin over the 8 XCDs).
+  const int G = args.n_mtiles * args.n_ntiles;
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7, i8 = wg >> 3;
+  const int per = G >> 3, rem = G & 7;
+  const int lin = xcd * per + min(xcd, rem) + i8;
+  const int mt = lin / args.n_ntiles, nt = lin % args.n_ntiles;
+  const int m0 = mt * kPM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4;
+
+  if (tid == 0) s_any = 0;
+  __syncthreads();
+  if (tid < kPM) {
+    // Without a mapping (plain linear) slot m0 + tid is row m0 + tid of A.
+    int tk = args.tp2id ? args.tp2id[m0 + tid] : m0 + tid;
+    if (tk < 0 || tk >= args.T) tk = -1;
+    stok[tid] = tk;
+    if (tk >= 0) s_any = 1;
+  }
+  __syncthreads();
+  if (!s_any) return;
+
+  const int e = args.b2e ? args.b2e[m0 / args.B] : 0;
+  const int K = args.K;
+  const size_t rg_bytes = (size_t)K * 8, rg_sbytes = (size_t)K / 2;
+  const int n_rg_total = args.N_rows / 16;
+  const int rg0 = nt * kPRG;
+  const int rg_valid = min(kPRG, n_rg_total - rg0);
+  const uint8_t* wq = args.wq + ((size_t)e * n_rg_total + rg0) * rg_bytes;
+  const uint8_t* ws = args.ws + ((size_t)e * n_rg_total + rg0) * rg_sbytes;
+  const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
+
+  // ---- global -> register staging assignment
+  // A: 4 pieces of 16 B per thread: row = 32*i + tid/16, col16 = tid%16
+  const int a_col = tid & 15, a_row0 = tid >> 4;
+  const uint16_t* a_src[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 32 * i + a_row0;
+    const int tk = stok[row];
+    if (tk < 0) a_src[i] = nullptr;
+    else if (GATE_UP) a_src[i] = args.a + (size_t)tk * K;
+    else a_src[i] = args.a + (size_t)(m0 + row) * K;
+  }
+  // B: 2 pieces of 16 B: rg = (tid + 512 i) / 64, l16 = tid % 64
+  const int b_l = tid & 63;
+  const int b_rg0 = tid >> 6;  // + 8 i
+  // S: threads < 256, 4 bytes: rg = tid / 16, b4 = tid % 16
+  const int s_rg = tid >> 4, s_b4 = tid & 15;
+
+  u32x4 ra[4], rbw[2];
+  uint32_t rs = 0;
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+
+  auto load_chunk = [&](int c) {
+    const int k0 = c * 128;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = k0 + a_col * 8;
+      ra[i] = (a_src[i] && kk < K) ? *reinterpret_cast<const u32x4*>(a_src[i] + kk) : zero4;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rg = b_rg0 + 8 * i;
+      const bool ok = rg < rg_valid && (c < nfull || (b_l >> 4) < tail_q);
+      rbw[i] = ok ? *reinterpret_cast<const u32x4*>(wq + rg * rg_bytes + (size_t)c * 1024 + b_l * 16)
+                  : zero4;
+    }
+    if (tid < 256) {
+      const bool ok = s_rg < rg_valid && (c < nfull || (s_b4 >> 2) < tail_q);
+      rs = ok ? *reinterpret_cast<const uint32_t*>(ws + s_rg * rg_sbytes + (size_t)c * 64 + s_b4 * 4)
+              : 0u;
+    }
+  };
+  auto store_chunk = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<u32x4*>(&sa[st][(32 * i + a_row0) * kARow + a_col * 16]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<u32x4*>(&sb[st][(b_rg0 + 8 * i) * 1024 + b_l * 16]) = rbw[i];
+    if (tid < 256) *reinterpret_cast<uint32_t*>(&ss[st][s_rg * 64 + s_b4 * 4]) = rs;
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  // Wave-uniform activity: its row groups exist and one of its 64 slots is real.
+  bool wave_rows = (4 * wn) < rg_valid;
+  bool wave_slots = false;
+  for (int i = 0; i < 64; ++i) wave_slots |= stok[64 * wm + i] >= 0;
+  const bool active = wave_rows && wave_slots;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (int c = 0; c < nc; ++c) {
+    const int st = c & 1;
+    if (c + 1 < nc) load_chunk(c + 1);
+    if (active) {
+      u32x4 wv[4];
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        wv[r] = *reinterpret_cast<const u32x4*>(&sb[st][(4 * wn + r) * 1024 + lane * 16]);
+        sc[r] = e8m0_to_f32(ss[st][(4 * wn + r) * 64 + lane]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4 xv[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          xv[t] = *reinterpret_cast<const u32x4*>(
+              &sa[st][(64 * wm + 16 * t + (lane & 15)) * kARow + (32 * q + 8 * j) * 2]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bf16x8 wf = dequant8(wv[r][j], sc[r]);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[r][t] = mfma16(wf, as_bf16x8(xv[t]), acc[r][t]);
+        }
+      }
+    }
+    if (c + 1 < nc) store_chunk(st ^ 1);
+    __syncthreads();
+  }
+  if (!active) return;
+
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  if (GATE_UP) {
+    const int I = args.I;
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      if (4 * wn + 2 * pp >= rg_valid) continue;
+      const int P = (rg0 + 4 * wn) / 2 + pp;  // pair index = 16 intermediate columns
+      const int col0 = 16 * P + 4 * q;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = 64 * wm + 16 * t + (lane & 15);
+        if (stok[row] < 0) continue;
+        const f32x4 g4 = acc[2 * pp][t], u4 = acc[2 * pp + 1][t];
+        uint16_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float g = rb(g4[i]), u = rb(u4[i]);
+          if (args.bias) {
+            g = rb(g + bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + col0 + i]));
+            u = rb(u + bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + I + col0 + i]));
+          }
+          g = clamp_ref(g, args.p.gate_lo, args.p.gate_hi);
+          u = clamp_ref(u, args.p.up_lo, args.p.up_hi);
+          h[i] = f32_to_bf16_bits(u * act_bf16(g, args.p.act));
+        }
+        *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * I + col0) =
+            u16x4{h[0], h[1], h[2], h[3]};
+      }
+    }
+  } else {
+    const int H = args.H;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (4 * wn + r >= rg_valid) continue;
+      const int n0 = 16 * (rg0 + 4 * wn + r) + 4 * q;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = 64 * wm + 16 * t + (lane & 15);
+        if (stok[row] < 0) continue;
+        uint16_t y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = rb(acc[r][t][i]);
+          if (args.bias) v = rb(v + bf16_bits_to_f32(args.bias[(size_t)e * H + n0 + i]));
+          y[i] = f32_to_bf16_bits(v);
+        }
+        *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * H + n0) =
+            u16x4{y[0], y[1], y[2], y[3]};
+      }
+    }
+  }
+}
+
+// inv[t, e] = slot of (t, e) or -1.
+__global__ void cte_inverse_kernel(const int32_t* __restrict__ tp2id,
+                                   const int32_t* __restrict__ b2e, int64_t n_slots, int B, int T,
+                                   int E, int32_t* __restrict__ inv) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n_slots) return;
+  const int tk = tp2id[p];
+  if (tk < 0 || tk >= T) return;
+  const int e = b2e[p / B];
+  if (e < 0 || e >= E) return;
+  inv[(size_t)tk * E + e] = (int32_t)p;
+}
+
+// out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.
+__global__ void __launch_bounds__(256) cte_combine_kernel(const uint16_t* __restrict__ y,
+                                                          const int32_t* __restrict__ inv,
+                                                          const float* __restrict__ aff, int H,
+                                                          int E, int scale_mode,
+                                                          uint16_t* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= H) return;
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < E; ++e) {
+    const int p = inv[(size_t)t * E + e];
+    if (p < 0) continue;
+    float a = aff[(size_t)t * E + e];
+    if (scale_mode == MXMOE_SCALE_NO) a = 1.0f;
+    const u16x4 v = *reinterpret_cast<const u16x4*>(y + (size_t)p * H + n);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
+  }
+  *reinterpret_cast<u16x4*>(out + (size_t)t * H + n) =
+      u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
+            f32_to_bf16_bits(acc[3])};
+}
+
+__global__ void fill_i32_k(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+struct CteWs {
+  uint16_t* h;
+  uint16_t* y;
+  int32_t* inv;
+};
+
+static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
+                        int64_t n_slots, CteWs* w) {
+  Carver cv(base, cap);
+  CteWs c;
+  c.h = cv.take<uint16_t>(n_slots * I);
+  c.y = cv.take<uint16_t>(n_slots * H);
+  c.inv = cv.take<int32_t>(T * E);
+  if (w) *w = c;
+  return cv.off + 256;
+}
+
+}  // namespace mxmoe
+
+using namespace mxmoe;
+
+extern "C" size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                                int64_t block_size, int64_t n_blocks) {
+  return cte_carve(nullptr, ~(size_t)0, T, H, I, E, block_size * n_blocks, nullptr);
+}
+
+extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
+                             const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                             const uint8_t* dn_s, const uint16_t* gu_bias,
+                             const uint16_t* dn_bias, const int32_t* token_position_to_id,
+                             const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
+                             int64_t T, int64_t H, int64_t I, int64_t E, int act,
+                             const float* clamps, int scale_mode, uint16_t* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  clear_error();
+  MXMOE_REQUIRE(x && affinities_masked && gu_q && gu_s && dn_q && dn_s && token_position_to_id &&
+                    block_to_expert && out && workspace,
+                "moe_cte: null pointer");
+  MXMOE_REQUIRE(T >= 1 && E >= 1 && n_blocks >= 1, "moe_cte: bad T/E/n_blocks");
+  MXMOE_REQUIRE(block_size >= 128 && block_size % 128 == 0,
+                "moe_cte: block_size=%lld must be a multiple of 128", (long long)block_size);
+  MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
+                "moe_cte: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
+  MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_cte: unknown activation %d", act);
+  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
+                "moe_cte: unsupported scale mode %d", scale_mode);
+  const int64_t n_slots = n_blocks * block_size;
+  const size_t need = cte_carve(nullptr, ~(size_t)0, T, H, I, E, n_slots, nullptr);
+  if (workspace_bytes < need)
+    return set_error(MXMOE_E_WORKSPACE, "moe_cte: workspace %zu < %zu", workspace_bytes, need);
+  CteWs w;
+  cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, &w);
+  hipStream_t s = as_stream(stream);
+
+  PrefillArgs a;
+  a.tp2id = token_position_to_id;
+  a.b2e = block_to_expert;
+  a.T = (int)T;
+  a.I = (int)I;
+  a.H = (int)H;
+  a.B = (int)block_size;
+  a.n_mtiles = (int)(n_slots / kPM);
+  a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
+  a.p.gate_hi = clamps ? clamps[1] : INFINITY;
+  a.p.up_lo = clamps ? clamps[2] : -INFINITY;
+  a.p.up_hi = clamps ? clamps[3] : INFINITY;
+  a.p.act = act;
+
+  // gate_up: A = x (K = H), rows = 2I
+  a.a = x;
+  a.wq = gu_q;
+  a.ws = gu_s;
+  a.bias = gu_bias;
+  a.out = w.h;
+  a.K = (int)H;
+  a.N_rows = (int)(2 * I);
+  a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
+  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+                     dim3(kPThreads), 0, s, a);
+  // down: A = h (K = I), rows = H
+  a.a = w.h;
+  a.wq = dn_q;
+  a.ws = dn_s;
+  a.bias = dn_bias;
+  a.out = w.y;
+  a.K = (int)I;
+  a.N_rows = (int)H;
+  a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+                     dim3(kPThreads), 0, s, a);
+  hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
+                     T * E, -1);
+  hipLaunchKernelGGL(cte_inverse_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
+                     token_position_to_id, block_to_expert, n_slots, (int)block_size, (int)T,
+                     (int)E, w.inv);
+  hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
+                     dim3(256), 0, s, w.y, w.inv, affinities_masked, (int)H, (int)E, scale_mode,
+                     out);
+  return check_launch("moe_cte");
+}
+
+extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, const uint8_t* ws,
+                            int64_t N, int64_t K, uint16_t* y, void* stream) {
+  clear_error();
+  MXMOE_REQUIRE(x && wq && ws && y, "linear: null pointer");
+  MXMOE_REQUIRE(M >= 0 && N >= 16 && N % 16 == 0 && K >= 32 && K % 32 == 0,
+                "linear: N=%lld must be a multiple of 16 and K=%lld of 32", (long long)N,
+                (long long)K);
+  if (M == 0) return MXMOE_OK;
+  PrefillArgs a = {};
+  a.a = x;
+  a.wq = wq;
+  a.ws = ws;
+  a.out = y;
+  a.T = (int)M;
+  a.K = (int)K;
+  a.N_rows = (int)N;
+  a.H = (int)N;
+  a.I = 0;
+  a.B = kPM;
+  a.n_mtiles = (int)((M + kPM - 1) / kPM);
+  a.n_ntiles = (int)((N / 16 + kPRG - 1) / kPRG);
+  a.p.gate_lo = -INFINITY;
+  a.p.gate_hi = INFINITY;
+  a.p.up_lo = -INFINITY;
+  a.p.up_hi = INFINITY;
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+                     dim3(kPThreads), 0, as_stream(stream), a);
+  return check_launch("linear");
+}

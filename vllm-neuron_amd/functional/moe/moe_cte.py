@@ -1,0 +1,101 @@
+"""Prefill expert MLP (context encoding) on the MI355X kernel.
+
+Mirrors vllm_neuron/functional/moe/moe_cte.py:37-420 (signature, argument
+meaning, exception types).  The reference dispatches to nkilib moe_cte
+(shard_on_block_mx for MXFP4, :650-732) or, on CPU and for non-MX weights, its
+torch flow ``_torch_moe_impl`` (:448-581).  Here every call runs mxmoe_moe_cte:
+the blockwise grouped gate_up GEMM with fused MXFP4 dequant, bias, clamps and
+activation, the down GEMM with bias, and the affinity-weighted combine, with the
+bf16 intermediate roundings of ``_torch_moe_impl``.
+
+Weights are the packed MXFP4 layout of vllm_neuron_amd.weights (the reference's
+own MX layout is Trainium-specific): gate_up_proj_weight uint8 [E, 2I/16, 8H] with
+gate_up_proj_scale [E, 2I/16, H/2]; down_proj_weight [E, H/16, 8I] with
+down_proj_scale [E, H/16, I/2].  Trainium tuning arguments (n_block_per_iter,
+block_sharding_strategy, n_static_blocks, n_dynamic_blocks, checkpoint_activation,
+skip_weight, ...) are accepted and have no effect; ``conditions`` is not needed
+because empty blocks are detected from token_position_to_id.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+from torch import Tensor
+
+from ... import _lib
+from ...enums import MoECTEImplementation, QuantizationType, member_name
+from ._common import act_code, down_bias, expert_shapes, gate_up_bias, scale_code
+
+
+def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_proj_weight: Tensor,
+            down_proj_weight: Tensor, token_position_to_id: Tensor, block_to_expert: Tensor,
+            block_size: int, implementation=MoECTEImplementation.shard_on_block_mx,
+            n_block_per_iter: int = 1, block_sharding_strategy=None, n_static_blocks: int = -1,
+            n_dynamic_blocks: int = 55, checkpoint_activation: bool = False,
+            expert_affinity_multiply_on_I: bool = False, num_static_block: Optional[int] = None,
+            conditions: Optional[Tensor] = None, gate_and_up_proj_bias: Optional[Tensor] = None,
+            down_proj_bias: Optional[Tensor] = None, gate_up_proj_scale: Optional[Tensor] = None,
+            down_proj_scale: Optional[Tensor] = None,
+            gate_up_activations_T: Optional[Tensor] = None,
+            down_activations: Optional[Tensor] = None, activation_function="SiLU",
+            skip_token: bool = False, skip_weight: bool = False, compute_dtype: Any = None,
+            is_tensor_update_accumulating: bool = True,
+            expert_affinities_scaling_mode="POST_SCALE",
+            gate_clamp_upper_limit: Optional[float] = None,
+            gate_clamp_lower_limit: Optional[float] = None,
+            up_clamp_upper_limit: Optional[float] = None,
+            up_clamp_lower_limit: Optional[float] = None,
+            quantization_type=QuantizationType.NONE, gate_w_scale=None, up_w_scale=None,
+            down_w_scale=None, gate_up_in_scale=None, down_in_scale=None,
+            use_packed_scales: bool = False) -> Tensor:
+    """Returns the MoE output [T, H] in bf16, T = expert_affinities_masked.shape[0] / E."""
+    if member_name(quantization_type) == "STATIC_MX":
+        raise NotImplementedError("STATIC_MX (FP8 weights) has no MI355X kernel")
+    if gate_up_activations_T is not None or down_activations is not None:
+        raise NotImplementedError("activation checkpoint buffers are not supported")
+    if gate_up_proj_scale is None or down_proj_scale is None:
+        raise AssertionError(
+            "gate_up_proj_scale and down_proj_scale must be provided for MX quantized compute")
+    dev = _lib.require_cuda(hidden_states, expert_affinities_masked, gate_up_proj_weight,
+                            down_proj_weight, token_position_to_id, block_to_expert)
+    E, H, I = expert_shapes(gate_up_proj_weight, gate_up_proj_scale, down_proj_weight,
+                            down_proj_scale)
+    if hidden_states.dim() != 2 or hidden_states.shape[1] != H:
+        raise ValueError(f"hidden_states must be [T(+1), {H}], got {tuple(hidden_states.shape)}")
+    if hidden_states.dtype != torch.bfloat16:
+        raise NotImplementedError("hidden_states must be bfloat16")
+    if (gate_and_up_proj_bias is None) != (down_proj_bias is None):
+        raise ValueError("gate_and_up_proj_bias and down_proj_bias must both be provided or neither")
+    if block_size % 128 != 0:
+        raise ValueError(f"block_size must be a multiple of 128, got {block_size}")
+    if token_position_to_id.numel() % block_size != 0:
+        raise ValueError("len(token_position_to_id) must be divisible by block_size")
+    n_blocks = token_position_to_id.numel() // block_size
+    if block_to_expert.numel() != n_blocks:
+        raise ValueError(f"len(block_to_expert) must equal N = {n_blocks}")
+    T = expert_affinities_masked.shape[0] // E
+    if hidden_states.shape[0] < T:
+        raise ValueError(f"hidden_states has {hidden_states.shape[0]} rows, need >= {T}")
+    x = hidden_states.contiguous()
+    aff = expert_affinities_masked.reshape(-1).to(torch.float32).contiguous()
+    tp2id = token_position_to_id.reshape(-1).to(torch.int32).contiguous()
+    b2e = block_to_expert.reshape(-1).to(torch.int32).contiguous()
+    gub = gate_up_bias(gate_and_up_proj_bias, E, I)
+    dnb = down_bias(down_proj_bias, E, H)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks), dev)
+    clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
+                               up_clamp_lower_limit, up_clamp_upper_limit)
+    rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), gate_up_proj_weight.contiguous().data_ptr(),
+                         gate_up_proj_scale.contiguous().data_ptr(),
+                         down_proj_weight.contiguous().data_ptr(),
+                         down_proj_scale.contiguous().data_ptr(), _lib.ptr(gub), _lib.ptr(dnb),
+                         tp2id.data_ptr(), b2e.data_ptr(), n_blocks, block_size, T, H, I, E,
+                         act_code(activation_function), clamps,
+                         scale_code(expert_affinities_scaling_mode), out.data_ptr(),
+                         ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
+    _lib.check(rc, "mxmoe_moe_cte")
+    return out

@@ -1,0 +1,73 @@
+"""MXFP4 MoE expert layer: the calls GPT-OSS makes into the operator API.
+
+Counterpart of ``GptOssExperts`` (vllm_neuron/model/gpt_oss/model_mxfp4.py:841-1458
+for the MXFP4 device path, model_bf16.py:1199-1413 for the CPU path) restricted to
+the expert path at one GPU: the input is the already-normalized hidden state.
+  * prefill (model_bf16.py:1282-1413): router (softmax over the top-k logits, fp32)
+    -> build_blockwise_mapping (block 256) -> moe_cte (Swish, clamps gate <= limit,
+    up in [-limit + 1, limit + 1], POST_SCALE, skip_token);
+  * decode (model_bf16.py:1199-1252 through moe_block_tkg's expert part): router
+    top-k -> moe_tkg in fp32 arithmetic.
+Plain SwiGLU layers (no clamp, SiLU) use the same calls without clamps.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .functional.moe.moe_blockwise import build_blockwise_mapping
+from .functional.moe.moe_cte import moe_cte
+from .functional.moe.moe_tkg import moe_tkg_raw
+from .functional.moe.router import router_topk_raw
+from .weights import MXFP4Experts
+
+BLOCK_SIZE = 256  # model_mxfp4.py:937
+
+
+class MXFP4MoE:
+    def __init__(self, experts: MXFP4Experts, router_w: torch.Tensor,
+                 router_b: Optional[torch.Tensor], top_k: int,
+                 swiglu_limit: Optional[float] = 7.0, block_size: int = BLOCK_SIZE):
+        self.w = experts
+        self.router_w = router_w.contiguous()  # [E, H] bf16
+        self.router_b = router_b
+        self.top_k = top_k
+        self.block_size = block_size
+        self.limit = swiglu_limit
+        if swiglu_limit is None:
+            self.act = _lib.ACT_SILU
+            self.clamp_args = (None, None, None, None)
+        else:
+            self.act = _lib.ACT_SWISH
+            self.clamp_args = (None, swiglu_limit, -swiglu_limit + 1, swiglu_limit + 1)
+
+    @property
+    def E(self) -> int:
+        return self.w.E
+
+    def route(self, x: torch.Tensor):
+        return router_topk_raw(x, self.router_w, self.top_k, self.router_b, _lib.ROUTER_SOFTMAX,
+                               False, False, 0.0)
+
+    def prefill(self, x: torch.Tensor, padding_mask: Optional[torch.Tensor] = None):
+        aff, _, _, _ = self.route(x)
+        aff_m, tp2id, b2e, _ = build_blockwise_mapping(aff, self.E, self.top_k, self.block_size,
+                                                       padding_mask=padding_mask)
+        g_lo, g_hi, u_lo, u_hi = self.clamp_args
+        w = self.w
+        return moe_cte(x, aff_m, w.gu_q, w.dn_q, tp2id, b2e, self.block_size,
+                       gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                       gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                       activation_function="Swish" if self.act == _lib.ACT_SWISH else "SiLU",
+                       skip_token=True, expert_affinities_scaling_mode="POST_SCALE",
+                       gate_clamp_upper_limit=g_hi, gate_clamp_lower_limit=g_lo,
+                       up_clamp_upper_limit=u_hi, up_clamp_lower_limit=u_lo)
+
+    def decode(self, x: torch.Tensor):
+        _, _, idx, val = self.route(x)
+        w = self.w
+        return moe_tkg_raw(x, idx, val, w.gu_q, w.gu_s, w.dn_q, w.dn_s, w.gu_bias, w.dn_bias,
+                           self.act, _lib.clamps_array(*self.clamp_args), _lib.SCALE_POST)

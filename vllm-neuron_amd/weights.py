@@ -1,0 +1,171 @@
+"""Load-time weight preparation: checkpoint MXFP4 tensors -> the kernels' packed layout.
+
+The reference prepares its kernel-facing MXFP4 layout once at load
+(vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:243-885, a Trainium-specific
+tiling); this module is the MI355X counterpart.  Input is the OCP/HF checkpoint
+layout (vllm_neuron/model/gpt_oss/model_mxfp4.py:2069-2141):
+
+  gate_up_proj_blocks [E, 2I, H/32, 16] uint8, gate_up_proj_scales [E, 2I, H/32] uint8,
+  rows interleaved (row 2i = gate_i, row 2i+1 = up_i);
+  down_proj_blocks [E, H, I/32, 16], down_proj_scales [E, H, I/32];
+  gate_up_proj_bias [E, 2I] (interleaved), down_proj_bias [E, H].
+
+Packed layout of one [N, K] matrix (rows grouped by 16, K in 128-element chunks):
+  data  [N/16, 8K] bytes: chunk c of row group g at g*8K + c*1024; inside it the
+        16 bytes of lane l are row 16g + l%16, K-block 4c + l//16 (a partial last
+        chunk keeps only its lanes l < 16 * blocks_in_chunk);
+  scale [N/16, K/2] bytes: the E8M0 byte of that (row, K-block) at g*K/2 + c*64 + l.
+Fused gate_up matrices alternate 16-row groups of gate and up rows.
+
+Every function here is a pure layout transform (torch views/permutes) that runs on
+whatever device its inputs live on.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+
+def _pack_2d(blocks: torch.Tensor, scales: torch.Tensor):
+    """blocks [L, N, G, 16], scales [L, N, G] -> data [L, N/16, 256G], scale [L, N/16, 16G]."""
+    L, N, G, _ = blocks.shape
+    if N % 16:
+        raise ValueError(f"row count {N} must be a multiple of 16")
+    nrg, nfull, tq = N // 16, G // 4, G % 4
+    b = blocks.reshape(L, nrg, 16, G, 16)
+    s = scales.reshape(L, nrg, 16, G)
+    parts_d, parts_s = [], []
+    if nfull:
+        bf = b[:, :, :, :4 * nfull, :].reshape(L, nrg, 16, nfull, 4, 16)
+        parts_d.append(bf.permute(0, 1, 3, 4, 2, 5).reshape(L, nrg, nfull * 1024))
+        sf = s[:, :, :, :4 * nfull].reshape(L, nrg, 16, nfull, 4)
+        parts_s.append(sf.permute(0, 1, 3, 4, 2).reshape(L, nrg, nfull * 64))
+    if tq:
+        bt = b[:, :, :, 4 * nfull:, :]  # [L, rg, r, tq, byte]
+        parts_d.append(bt.permute(0, 1, 3, 2, 4).reshape(L, nrg, tq * 256))
+        st = s[:, :, :, 4 * nfull:]
+        parts_s.append(st.permute(0, 1, 3, 2).reshape(L, nrg, tq * 16))
+    return torch.cat(parts_d, -1).contiguous(), torch.cat(parts_s, -1).contiguous()
+
+
+def pack_mxfp4(blocks: torch.Tensor, scales: torch.Tensor):
+    """OCP blocks [..., N, K/32, 16] + scales [..., N, K/32] -> packed (data, scale)
+    with shapes [..., N/16, 8K] and [..., N/16, K/2]."""
+    if blocks.dtype != torch.uint8 or scales.dtype != torch.uint8:
+        raise TypeError("MXFP4 blocks and scales must be uint8")
+    lead = blocks.shape[:-3]
+    N, G = blocks.shape[-3], blocks.shape[-2]
+    if blocks.shape[-1] != 16 or tuple(scales.shape) != tuple(blocks.shape[:-1]):
+        raise ValueError("expected blocks [..., N, G, 16] and scales [..., N, G]")
+    d, s = _pack_2d(blocks.reshape(-1, N, G, 16), scales.reshape(-1, N, G))
+    return d.reshape(*lead, N // 16, G * 256), s.reshape(*lead, N // 16, G * 16)
+
+
+def unpack_mxfp4(data: torch.Tensor, scale: torch.Tensor):
+    """Inverse of pack_mxfp4: packed [..., N/16, 8K] + [..., N/16, K/2] -> OCP blocks/scales."""
+    lead = data.shape[:-2]
+    nrg, nbytes = data.shape[-2], data.shape[-1]
+    G = nbytes // 256
+    nfull, tq = G // 4, G % 4
+    d = data.reshape(-1, nrg, nbytes)
+    s = scale.reshape(-1, nrg, G * 16)
+    L = d.shape[0]
+    outs_b, outs_s = [], []
+    if nfull:
+        bf = d[:, :, :nfull * 1024].reshape(L, nrg, nfull, 4, 16, 16)  # rg, c, q, r, byte
+        outs_b.append(bf.permute(0, 1, 4, 2, 3, 5).reshape(L, nrg, 16, nfull * 4, 16))
+        sf = s[:, :, :nfull * 64].reshape(L, nrg, nfull, 4, 16)
+        outs_s.append(sf.permute(0, 1, 4, 2, 3).reshape(L, nrg, 16, nfull * 4))
+    if tq:
+        bt = d[:, :, nfull * 1024:].reshape(L, nrg, tq, 16, 16)  # rg, tq, r, byte
+        outs_b.append(bt.permute(0, 1, 3, 2, 4))
+        st = s[:, :, nfull * 64:].reshape(L, nrg, tq, 16)
+        outs_s.append(st.permute(0, 1, 3, 2))
+    b = torch.cat(outs_b, 3).reshape(*lead, nrg * 16, G, 16)
+    sc = torch.cat(outs_s, 3).reshape(*lead, nrg * 16, G)
+    return b.contiguous(), sc.contiguous()
+
+
+def interleave_row_groups(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """[E, I, ...] gate and up rows -> [E, 2I, ...] alternating 16-row groups."""
+    E, I = gate.shape[:2]
+    rest = gate.shape[2:]
+    g = gate.reshape(E, I // 16, 1, 16, *rest)
+    u = up.reshape(E, I // 16, 1, 16, *rest)
+    return torch.cat([g, u], 2).reshape(E, 2 * I, *rest)
+
+
+def deinterleave_rows(t: torch.Tensor):
+    """Checkpoint gate_up rows (2i = gate_i, 2i+1 = up_i) -> (gate, up) along dim 1."""
+    return t[:, 0::2], t[:, 1::2]
+
+
+def gate_up_bias_from_checkpoint(bias: torch.Tensor, up_offset: float = 1.0) -> torch.Tensor:
+    """Checkpoint gate_up bias [E, 2I] (interleaved) -> [E, 2, I] = (gate, up + up_offset),
+    the +1 added in the bias dtype as the reference loader does
+    (weight_loaders_bf16.py:393-422; model_mxfp4.py:1104 passes hidden_act_bias=1.0)."""
+    gate = bias[:, 0::2]
+    up = bias[:, 1::2].clone()
+    if up_offset:
+        up = up + up_offset
+    return torch.stack([gate, up], 1).contiguous()
+
+
+@dataclass
+class MXFP4Experts:
+    """Packed expert weights of one MoE layer (all tensors on one device).
+
+    gu_q [E, 2I/16, 8H], gu_s [E, 2I/16, H/2]  fused gate_up (row groups alternate gate/up)
+    dn_q [E, H/16, 8I],  dn_s [E, H/16, I/2]   down projection
+    gu_bias [E, 2, I] bf16 (up half already holds +1 for GPT-OSS) or None
+    dn_bias [E, H] bf16 or None
+    """
+
+    gu_q: torch.Tensor
+    gu_s: torch.Tensor
+    dn_q: torch.Tensor
+    dn_s: torch.Tensor
+    gu_bias: Optional[torch.Tensor]
+    dn_bias: Optional[torch.Tensor]
+    E: int
+    H: int
+    I: int
+
+    @classmethod
+    def from_split(cls, gate_blocks, gate_scales, up_blocks, up_scales, down_blocks, down_scales,
+                   gu_bias=None, dn_bias=None):
+        """gate/up blocks [E, I, H/32, 16] (+ scales [E, I, H/32]); down [E, H, I/32, 16]."""
+        E, I, Gh = gate_blocks.shape[:3]
+        H = Gh * 32
+        gu_b = interleave_row_groups(gate_blocks, up_blocks)
+        gu_sc = interleave_row_groups(gate_scales, up_scales)
+        gu_q, gu_s = pack_mxfp4(gu_b, gu_sc)
+        dn_q, dn_s = pack_mxfp4(down_blocks, down_scales)
+        return cls(gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, E, H, I)
+
+    @classmethod
+    def from_checkpoint(cls, gate_up_blocks, gate_up_scales, down_blocks, down_scales,
+                        gate_up_bias=None, down_bias=None, up_bias_offset: float = 1.0):
+        """HF GPT-OSS tensors (interleaved gate/up rows) -> packed experts."""
+        gb, ub = deinterleave_rows(gate_up_blocks)
+        gs, us = deinterleave_rows(gate_up_scales)
+        gub = None if gate_up_bias is None else gate_up_bias_from_checkpoint(gate_up_bias,
+                                                                             up_bias_offset)
+        return cls.from_split(gb, gs, ub, us, down_blocks, down_scales, gub, down_bias)
+
+    def to(self, device):
+        mv = lambda t: None if t is None else t.to(device)  # noqa: E731
+        return MXFP4Experts(mv(self.gu_q), mv(self.gu_s), mv(self.dn_q), mv(self.dn_s),
+                            mv(self.gu_bias), mv(self.dn_bias), self.E, self.H, self.I)
+
+    def nbytes_per_expert(self) -> int:
+        n = (self.gu_q[0].numel() + self.gu_s[0].numel() + self.dn_q[0].numel()
+             + self.dn_s[0].numel())
+        if self.gu_bias is not None:
+            n += self.gu_bias[0].numel() * self.gu_bias.element_size()
+        if self.dn_bias is not None:
+            n += self.dn_bias[0].numel() * self.dn_bias.element_size()
+        return int(n)
