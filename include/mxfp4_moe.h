@@ -132,7 +132,9 @@ int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* padding_mask
  * -> nkilib moe_cte shard_on_block_mx); semantics of the torch flow at :448-581.
  * x bf16 [>=T, H]; affinities_masked fp32 [T*E]; gu_q/gu_s packed [E][2I x H];
  * dn_q/dn_s packed [E][H x I]; gu_bias bf16 [E, 2, I] or NULL; dn_bias bf16 [E, H]
- * or NULL; out bf16 [T, H].
+ * or NULL; out [T, H] in bf16, or fp32 when out_f32 = 1 (the dtype of the reference
+ * torch flow's result).  stage_events: NULL, or 4 hipEvent_t recorded on the stream
+ * before the gate_up GEMM, after it, after the down GEMM and after the combine.
  */
 size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                      int64_t block_size, int64_t n_blocks);
@@ -141,8 +143,9 @@ int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked, const uint8
                   const uint16_t* gu_bias, const uint16_t* dn_bias,
                   const int32_t* token_position_to_id, const int32_t* block_to_expert,
                   int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I,
-                  int64_t E, int act, const float* clamps, int scale_mode, uint16_t* out,
-                  void* workspace, size_t workspace_bytes, void* stream);
+                  int64_t E, int act, const float* clamps, int scale_mode, int out_f32,
+                  void* out, void* workspace, size_t workspace_bytes, void* const* stage_events,
+                  void* stream);
 
 /*
  * Decode expert MLP given routing: weight-streaming grouped GEMMs over the selected
@@ -153,6 +156,8 @@ int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked, const uint8
  * of the torch flow at moe_block_tkg.py:223-297.
  * x bf16 [T, H]; topk_idx int32 [T, k]; topk_val fp32 [T, k] (the affinity of each
  * selected expert); expert ids outside [0, E) are skipped (expert parallelism).
+ * stage_events: NULL, or 5 hipEvent_t recorded on the stream before the routing
+ * kernel, after it, after the gate_up kernel, after the down kernel, after the combine.
  */
 size_t mxmoe_moe_tkg_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k);
 int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
@@ -160,7 +165,7 @@ int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_
                   const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
                   int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
                   const float* clamps, int scale_mode, uint16_t* out, void* workspace,
-                  size_t workspace_bytes, void* stream);
+                  size_t workspace_bytes, void* const* stage_events, void* stream);
 
 /*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour

@@ -46,10 +46,11 @@ def test_argument_errors_are_reported():
                                      None, dummy, 1 << 20, None)
     assert rc == -1 and b"n_blocks" in lib.mxmoe_last_error()
     rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, dummy, dummy, 4,
-                           100, 64, 2880, 2880, 8, 2, None, 0, dummy, dummy, 1 << 30, None)
+                           100, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30, None,
+                           None)
     assert rc == -1 and b"block_size" in lib.mxmoe_last_error()
     rc = lib.mxmoe_moe_tkg(dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, None, 4, 2880,
-                           2880, 32, 4, 2, None, 0, dummy, dummy, 10, None)
+                           2880, 32, 4, 2, None, 0, dummy, dummy, 10, None, None)
     assert rc == -3 and b"workspace" in lib.mxmoe_last_error()
 
 

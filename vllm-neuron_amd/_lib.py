@@ -39,10 +39,10 @@ _SIGNATURES = {
                                      _SZ, _P]),
     "mxmoe_moe_cte_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                           _I64, _I, _P, _I, _P, _P, _SZ, _P]),
+                           _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
     "mxmoe_moe_tkg_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
-                           _I, _P, _P, _SZ, _P]),
+                           _I, _P, _P, _SZ, _P, _P]),
     "mxmoe_probe_hw_dequant": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_probe_mfma": (_I, [_P, _P, _P, _P]),
 }
@@ -115,6 +115,16 @@ def require_cuda(*tensors) -> torch.device:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def event_array(events):
+    """torch.cuda.Event list -> a C array of their hipEvent_t handles (or None)."""
+    if not events:
+        return None
+    for e in events:
+        if not e.cuda_event:  # torch creates the HIP event on its first record
+            e.record()
+    return (C.c_void_p * len(events))(*[e.cuda_event for e in events])
 
 
 def clamps_array(gate_lo, gate_hi, up_lo, up_hi):

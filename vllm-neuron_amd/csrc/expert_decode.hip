@@ -374,7 +374,7 @@ extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const f
                              const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
                              int top_k, int act, const float* clamps, int scale_mode,
                              uint16_t* out, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             void* const* stage_events, void* stream) {
   clear_error();
   MXMOE_REQUIRE(x && topk_idx && topk_val && gu_q && gu_s && dn_q && dn_s && out && workspace,
                 "moe_tkg: null pointer");
@@ -400,9 +400,14 @@ extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const f
   p.up_hi = clamps ? clamps[3] : INFINITY;
   p.act = act;
   hipStream_t s = as_stream(stream);
+  auto mark = [&](int i) {
+    if (stage_events) hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), s);
+  };
+  mark(0);
   hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
                      top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
                      w.tok_slot, w.tok_w);
+  mark(1);
   const int64_t maxne = T;  // an expert sees each token at most once
   const dim3 g1((unsigned)(I / 16), (unsigned)E), g2((unsigned)(H / 32), (unsigned)E);
 #define MXMOE_TKG_LAUNCH(NT)                                                                 \
@@ -410,8 +415,10 @@ extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const f
     hipLaunchKernelGGL((tkg_gate_up_kernel<NT>), g1, dim3(256), 0, s, x, (int)H, (int)I, gu_q, \
                        gu_s, gu_bias, w.expert_off, w.active, w.n_active, w.slot_tok, p,     \
                        w.h_hi, w.h_lo);                                                      \
+    mark(2);                                                                                 \
     hipLaunchKernelGGL((tkg_down_kernel<NT>), g2, dim3(256), 0, s, w.h_hi, w.h_lo, (int)H,     \
                        (int)I, dn_q, dn_s, dn_bias, w.expert_off, w.active, w.n_active, w.y); \
+    mark(3);                                                                                 \
   } while (0)
   if (maxne <= 16) MXMOE_TKG_LAUNCH(1);
   else if (maxne <= 32) MXMOE_TKG_LAUNCH(2);
@@ -419,5 +426,6 @@ extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const f
 #undef MXMOE_TKG_LAUNCH
   hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
                      dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, out);
+  mark(4);
   return check_launch("moe_tkg");
 }

@@ -273,8 +273,8 @@ __global__ void cte_inverse_kernel(const int32_t* __restrict__ tp2id,
 __global__ void __launch_bounds__(256) cte_combine_kernel(const uint16_t* __restrict__ y,
                                                           const int32_t* __restrict__ inv,
                                                           const float* __restrict__ aff, int H,
-                                                          int E, int scale_mode,
-                                                          uint16_t* __restrict__ out) {
+                                                          int E, int scale_mode, int out_f32,
+                                                          void* __restrict__ out) {
   const int t = blockIdx.y;
   const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= H) return;
@@ -289,9 +289,13 @@ __global__ void __launch_bounds__(256) cte_combine_kernel(const uint16_t* __rest
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
   }
-  *reinterpret_cast<u16x4*>(out + (size_t)t * H + n) =
-      u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
-            f32_to_bf16_bits(acc[3])};
+  if (out_f32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (size_t)t * H + n) = acc;
+  } else {
+    *reinterpret_cast<u16x4*>(static_cast<uint16_t*>(out) + (size_t)t * H + n) =
+        u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
+              f32_to_bf16_bits(acc[3])};
+  }
 }
 
 __global__ void fill_i32_k(int32_t* __restrict__ p, int64_t n, int32_t v) {
@@ -331,8 +335,9 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                              const uint16_t* dn_bias, const int32_t* token_position_to_id,
                              const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
                              int64_t T, int64_t H, int64_t I, int64_t E, int act,
-                             const float* clamps, int scale_mode, uint16_t* out, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             const float* clamps, int scale_mode, int out_f32, void* out,
+                             void* workspace, size_t workspace_bytes, void* const* stage_events,
+                             void* stream) {
   clear_error();
   MXMOE_REQUIRE(x && affinities_masked && gu_q && gu_s && dn_q && dn_s && token_position_to_id &&
                     block_to_expert && out && workspace,
@@ -352,6 +357,9 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   CteWs w;
   cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, &w);
   hipStream_t s = as_stream(stream);
+  auto mark = [&](int i) {
+    if (stage_events) hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), s);
+  };
 
   PrefillArgs a;
   a.tp2id = token_position_to_id;
@@ -376,8 +384,10 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
+  mark(0);
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
                      dim3(kPThreads), 0, s, a);
+  mark(1);
   // down: A = h (K = I), rows = H
   a.a = w.h;
   a.wq = dn_q;
@@ -389,6 +399,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
   hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
                      dim3(kPThreads), 0, s, a);
+  mark(2);
   hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
                      T * E, -1);
   hipLaunchKernelGGL(cte_inverse_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
@@ -396,7 +407,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                      (int)E, w.inv);
   hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
                      dim3(256), 0, s, w.y, w.inv, affinities_masked, (int)H, (int)E, scale_mode,
-                     out);
+                     out_f32, out);
+  mark(3);
   return check_launch("moe_cte");
 }
 

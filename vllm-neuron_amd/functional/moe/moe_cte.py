@@ -49,8 +49,15 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
             up_clamp_lower_limit: Optional[float] = None,
             quantization_type=QuantizationType.NONE, gate_w_scale=None, up_w_scale=None,
             down_w_scale=None, gate_up_in_scale=None, down_in_scale=None,
-            use_packed_scales: bool = False) -> Tensor:
-    """Returns the MoE output [T, H] in bf16, T = expert_affinities_masked.shape[0] / E."""
+            use_packed_scales: bool = False, output_dtype: torch.dtype = torch.bfloat16,
+            stage_events=None) -> Tensor:
+    """Returns the MoE output [T, H], T = expert_affinities_masked.shape[0] / E, in
+    ``output_dtype``: bf16 (default, the device kernel's result) or float32 (the dtype
+    of the reference torch flow, which promotes through the fp32 affinities).
+    ``stage_events``: optional 4 torch.cuda.Event (enable_timing) recorded around the
+    gate_up GEMM, the down GEMM and the combine."""
+    if output_dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("output_dtype must be bfloat16 or float32")
     if member_name(quantization_type) == "STATIC_MX":
         raise NotImplementedError("STATIC_MX (FP8 weights) has no MI355X kernel")
     if gate_up_activations_T is not None or down_activations is not None:
@@ -84,7 +91,7 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
     b2e = block_to_expert.reshape(-1).to(torch.int32).contiguous()
     gub = gate_up_bias(gate_and_up_proj_bias, E, I)
     dnb = down_bias(down_proj_bias, E, H)
-    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(T, H, dtype=output_dtype, device=dev)
     L = _lib.lib()
     ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks), dev)
     clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
@@ -95,7 +102,8 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
                          down_proj_scale.contiguous().data_ptr(), _lib.ptr(gub), _lib.ptr(dnb),
                          tp2id.data_ptr(), b2e.data_ptr(), n_blocks, block_size, T, H, I, E,
                          act_code(activation_function), clamps,
-                         scale_code(expert_affinities_scaling_mode), out.data_ptr(),
-                         ws.data_ptr(), ws.numel(), _lib.stream_handle(dev))
+                         scale_code(expert_affinities_scaling_mode),
+                         int(output_dtype == torch.float32), out.data_ptr(), ws.data_ptr(),
+                         ws.numel(), _lib.event_array(stage_events), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_cte")
     return out

@@ -25,8 +25,10 @@ from ._common import act_code, down_bias, expert_shapes, gate_up_bias, scale_cod
 
 
 def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, gu_q, gu_s, dn_q, dn_s, gub, dnb,
-                act: int, clamps, scale_mode: int) -> Tensor:
-    """Kernel call: x bf16 [T, H], topk_idx int32 [T, k] (local ids), topk_val fp32 [T, k]."""
+                act: int, clamps, scale_mode: int, stage_events=None) -> Tensor:
+    """Kernel call: x bf16 [T, H], topk_idx int32 [T, k] (local ids), topk_val fp32 [T, k].
+    stage_events: optional 5 torch.cuda.Event recorded around routing, gate_up, down and
+    combine."""
     dev = _lib.require_cuda(x, topk_idx, topk_val, gu_q)
     E, H, I = expert_shapes(gu_q, gu_s, dn_q, dn_s)
     T, K = topk_idx.shape
@@ -37,7 +39,7 @@ def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, gu_q, gu_s, dn_q,
                          topk_val.contiguous().data_ptr(), gu_q.data_ptr(), gu_s.data_ptr(),
                          dn_q.data_ptr(), dn_s.data_ptr(), _lib.ptr(gub), _lib.ptr(dnb), T, H, I,
                          E, K, act, clamps, scale_mode, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                         _lib.stream_handle(dev))
+                         _lib.event_array(stage_events), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_tkg")
     return out
 

@@ -52,7 +52,8 @@ class MXFP4MoE:
         return router_topk_raw(x, self.router_w, self.top_k, self.router_b, _lib.ROUTER_SOFTMAX,
                                False, False, 0.0)
 
-    def prefill(self, x: torch.Tensor, padding_mask: Optional[torch.Tensor] = None):
+    def prefill(self, x: torch.Tensor, padding_mask: Optional[torch.Tensor] = None,
+                output_dtype: torch.dtype = torch.bfloat16, stage_events=None):
         aff, _, _, _ = self.route(x)
         aff_m, tp2id, b2e, _ = build_blockwise_mapping(aff, self.E, self.top_k, self.block_size,
                                                        padding_mask=padding_mask)
@@ -64,10 +65,12 @@ class MXFP4MoE:
                        activation_function="Swish" if self.act == _lib.ACT_SWISH else "SiLU",
                        skip_token=True, expert_affinities_scaling_mode="POST_SCALE",
                        gate_clamp_upper_limit=g_hi, gate_clamp_lower_limit=g_lo,
-                       up_clamp_upper_limit=u_hi, up_clamp_lower_limit=u_lo)
+                       up_clamp_upper_limit=u_hi, up_clamp_lower_limit=u_lo,
+                       output_dtype=output_dtype, stage_events=stage_events)
 
-    def decode(self, x: torch.Tensor):
+    def decode(self, x: torch.Tensor, stage_events=None):
         _, _, idx, val = self.route(x)
         w = self.w
         return moe_tkg_raw(x, idx, val, w.gu_q, w.gu_s, w.dn_q, w.dn_s, w.gu_bias, w.dn_bias,
-                           self.act, _lib.clamps_array(*self.clamp_args), _lib.SCALE_POST)
+                           self.act, _lib.clamps_array(*self.clamp_args), _lib.SCALE_POST,
+                           stage_events)
