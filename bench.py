@@ -59,6 +59,7 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=None)
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time decode with eager launches")
     return ap.parse_args()
 
 
@@ -176,32 +177,76 @@ def main():
     for s in range(args.warmup):
         layers[s % L].decode(xs[s % L])
     torch.cuda.synchronize()
-    steps = args.steps
-    stage = [[ev() for _ in range(5)] for _ in range(steps)]
-    t0, t1 = ev(), ev()
-    torch.cuda.synchronize()
-    t0.record()
-    for s in range(steps):
+
+    # Per-kernel durations: an eager pass with the library's stage events on the launch
+    # stream (events recorded inside a captured graph do not time its kernels).
+    n_ev = min(args.steps, 100)
+    stage = [[ev() for _ in range(6)] for _ in range(n_ev)]
+    e0, e1 = ev(), ev()
+    e0.record()
+    for s in range(n_ev):
         layers[s % L].decode(xs[s % L], stage_events=stage[s])
-    t1.record()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / n_ev
+
+    steps = args.steps
+    mode = "eager"
+    if not args.no_graph:
+        # One graph holds G consecutive steps (each layer G / L times); the timed region
+        # replays it, so ``steps`` is rounded to a multiple of G.
+        G = min(steps, 5 * L)
+        reps = max(1, steps // G)
+        steps = G * reps
+        try:
+            graph = torch.cuda.CUDAGraph()
+            cap_stream = torch.cuda.Stream()
+            cap_stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(cap_stream):
+                with torch.cuda.graph(graph, stream=cap_stream):
+                    for s in range(G):
+                        layers[s % L].decode(xs[s % L])
+            torch.cuda.current_stream().wait_stream(cap_stream)
+            graph.replay()
+            torch.cuda.synchronize()
+            mode = "hip-graph"
+        except Exception as exc:  # capture unsupported: time eagerly
+            print(f"graph capture failed ({exc}); timing eagerly", file=sys.stderr)
+            torch.cuda.synchronize()
+    t0, t1 = ev(), ev()
+    if mode == "hip-graph":
+        t0.record()
+        for _ in range(reps):
+            graph.replay()
+        t1.record()
+    else:
+        t0.record()
+        for s in range(steps):
+            layers[s % L].decode(xs[s % L])
+        t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
-    gu_ms = sum(stage[s][1].elapsed_time(stage[s][2]) for s in range(steps)) / steps
-    dn_ms = sum(stage[s][2].elapsed_time(stage[s][3]) for s in range(steps)) / steps
-    rt_ms = sum(stage[s][0].elapsed_time(stage[s][1]) for s in range(steps)) / steps
-    cb_ms = sum(stage[s][3].elapsed_time(stage[s][4]) for s in range(steps)) / steps
+
+    def stage_ms(a, b):
+        return sum(stage[s][a].elapsed_time(stage[s][b]) for s in range(n_ev)) / n_ev
+
+    rt_ms, route_ms, gu_ms = stage_ms(0, 1), stage_ms(1, 2), stage_ms(2, 3)
+    dn_ms, cb_ms = stage_ms(3, 4), stage_ms(4, 5)
     avg_touched = sum(touched[s % L] for s in range(steps)) / steps
     bpe = bytes_per_expert(H, I, biases)
     layer_bytes = avg_touched * bpe + E * H * 2 + 2 * dT * H * 2
-    gu_bytes = avg_touched * gate_up_bytes_per_expert(H, I, biases) + dT * H * 2
+    # the roofline kernel's duration comes from the eager pass over n_ev steps
+    ev_touched = sum(touched[s % L] for s in range(n_ev)) / n_ev
+    gu_bytes = ev_touched * gate_up_bytes_per_expert(H, I, biases) + dT * H * 2
     decode = {
         "tokens_per_s": dT / (ms * 1e-3), "ms_per_step": ms,
         "experts_touched_avg": avg_touched,
         "layer_algorithmic_bytes": layer_bytes,
         "layer_GBps": layer_bytes / (ms * 1e-3) / 1e9,
         "layer_frac_hbm": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "kernel_ms": {"router+topk+route": rt_ms, "gate_up": gu_ms, "down": dn_ms,
+        "kernel_ms": {"router": rt_ms, "route": route_ms, "gate_up": gu_ms, "down": dn_ms,
                       "combine": cb_ms},
+        "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
     }
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "kernel": "tkg_gate_up_kernel", "achieved": gu_gbs,

@@ -168,6 +168,25 @@ int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_
                   size_t workspace_bytes, void* const* stage_events, void* stream);
 
 /*
+ * Whole decode expert layer in one call: router (as mxmoe_router_topk) on x, then the
+ * mxmoe_moe_tkg pipeline on the selected experts.  The counterpart of the router +
+ * expert stages of nkilib moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512)
+ * for an already-normalized input; semantics of moe_block_tkg.py:152-297.
+ * router_w bf16 [E, H], router_b bf16 [E] or NULL; logits_out fp32 [T, E] or NULL.
+ * stage_events: NULL, or 6 hipEvent_t recorded before the router and after the router,
+ * routing, gate_up, down and combine kernels.
+ */
+size_t mxmoe_moe_decode_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k);
+int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
+                     int router_act, int act_before_topk, int renorm, float renorm_eps,
+                     const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                     const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
+                     int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
+                     const float* clamps, int scale_mode, uint16_t* out, float* logits_out,
+                     void* workspace, size_t workspace_bytes, void* const* stage_events,
+                     void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour
  * the kernels rely on.  mxmoe_probe_hw_dequant runs the CDNA4 scaled fp4->bf16
  * conversion the GEMMs use over blocks/scales like mxmoe_dequant_bf16;

@@ -24,6 +24,17 @@ inline int check_launch(const char* what) {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Profiling marks: ev is null or an array of hipEvent_t handles supplied by the caller.
+inline void mark_event(void* const* ev, int i, hipStream_t s) {
+  if (ev) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
+}
+
+// Router logits + top-k + activation (router.hip); affinities may be null.
+int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64_t T, int64_t H,
+               int64_t E, int top_k, int act, int act_before_topk, int renorm, float renorm_eps,
+               float* logits, float* affinities, int32_t* topk_idx, float* topk_val,
+               hipStream_t s);
+
 // Bump allocator over a caller-provided workspace.
 struct Carver {
   char* base;

@@ -36,6 +36,12 @@ constexpr int kChunkK = 128;       // K elements per chunk
 constexpr int kChunkBytes = 1024;  // data bytes per chunk of a row group
 constexpr int kRowGroup = 16;
 
+// Wave index inside the workgroup as a wave-uniform (scalar) value, so branches
+// on it stay scalar instead of turning into EXEC-mask divergence.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }

@@ -3,12 +3,14 @@
 //
 //   route      one workgroup: per-expert slot lists (tokens ascending inside an
 //              expert), the list of active experts, per-token slots sorted by expert
-//   gate_up    grid (I/16 column pairs, active experts); a workgroup streams one
-//              16-row gate group and the matching 16-row up group over all of K,
-//              its 4 waves splitting K chunks; fused bias, clamps, activation;
-//              the fp32 activation is stored as a bf16 hi/lo pair
-//   down       grid (H/32, active experts); two MFMAs (hi, lo) per product
+//   gate_up    streaming kernel, one wave per item (active expert, 4 row groups =
+//              2 gate/up pairs): the item's packed weights stream over all of K
+//              through a register ring of D chunks; fused bias, clamps and
+//              activation; the fp32 activation is stored as a bf16 (hi, lo) pair
+//   down       the same streaming kernel over (active expert, 4 row groups of H); two
+//              MFMAs (hi, lo) per product, fp32 bias
 //   combine    out[t] = bf16(sum over the token's experts in ascending id of y * w)
+// Items are independent and each writes its own outputs.
 #include <math.h>
 
 #include "capi_util.h"
@@ -133,181 +135,235 @@ __device__ __forceinline__ float act_f32(float g, int act) {
   return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
 }
 
-// One wave's share of a streamed GEMM tile: R row groups (A = weights) times NT
-// token tiles (B = activations) over chunks c = c0, c0 + cs, ...
-// brow[t] points at this lane's activation row of token tile t (bf16, length K),
-// or is null for a token past the expert's list.  With SPLIT the activations come
-// as (hi, lo) pairs: brow2 points at the lo rows.
+// Registers of one K chunk of a streamed tile: R weight row groups (16 B + one
+// scale byte per lane each) and NT token tiles of activations (4 x 16 B per lane;
+// with SPLIT a second (lo) copy).
 template <int R, int NT, bool SPLIT>
-__device__ __forceinline__ void stream_wave(const uint8_t* __restrict__ wq,
-                                            const uint8_t* __restrict__ ws, size_t rg_bytes,
-                                            size_t rg_sbytes, const uint16_t* const* brow,
-                                            const uint16_t* const* brow2, int ntv, int K, int c0,
-                                            int cs, f32x4 (&acc)[R][NT]) {
+struct ChunkFrag {
+  u32x4 w[R];
+  uint32_t s[R];
+  u32x4 b[NT][4];
+  u32x4 b2[SPLIT ? NT : 1][4];
+};
+
+struct StreamGeom {
+  const uint8_t* wq;  // first row group of the tile
+  const uint8_t* ws;
+  size_t rg_bytes, rg_sbytes;
+  int rv;             // valid row groups in the tile (<= R)
+  int nfull, tail_q;  // full 128-wide chunks, 32-blocks in the partial last chunk
+};
+
+// Plain loads only, so nothing waits on them before their use: lanes past K in a
+// partial last chunk re-read lane 0's bytes of the same chunk, row groups past the
+// tile re-read its last valid one, and lanes of absent tokens read a valid row of
+// the expert (the same address as their neighbours, so the requests coalesce).
+// mma_chunk gives the lanes past K a zero scale, so their weights dequantize to
+// exact zeros; row groups past the tile and columns of absent tokens are computed
+// and never stored.
+template <int R, int NT, bool SPLIT>
+__device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, const StreamGeom& g,
+                                           const char* b1, const char* b2,
+                                           const uint32_t* row_off) {
   const int lane = threadIdx.x & 63, q = lane >> 4;
-  const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  for (int c = c0; c < nc; c += cs) {
-    const bool ok = (c < nfull) || (q < tail_q);
-    u32x4 wv[R];
-    uint32_t sv[R];
+  const bool ok = (c < g.nfull) || (q < g.tail_q);
+  const uint32_t lo = ok ? (uint32_t)lane : 0u;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      wv[r] = ok ? *reinterpret_cast<const u32x4*>(wq + r * rg_bytes + (size_t)c * 1024 + lane * 16)
-                 : zero4;
-      sv[r] = ok ? (uint32_t)ws[r * rg_sbytes + (size_t)c * 64 + lane] : 0u;
-    }
-    const int k0 = c * 128 + q * 32;
-    u32x4 bv[NT][4], bv2[NT][4];
+  for (int r = 0; r < R; ++r) {
+    const int rr = r < g.rv ? r : g.rv - 1;
+    const uint8_t* wb = g.wq + rr * g.rg_bytes + (size_t)c * 1024;  // wave-uniform
+    const uint8_t* sb = g.ws + rr * g.rg_sbytes + (size_t)c * 64;
+    // Weights are read once per step: non-temporal, so they do not evict the
+    // activations and scales that neighbouring waves re-read from the caches.
+    f.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + lo * 16u));
+    f.s[r] = sb[lo];
+  }
+  const uint32_t k0b = ok ? (uint32_t)(c * 128 + q * 32) * 2u : 0u;  // byte offset in a row
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const bool tv = ok && brow[t] != nullptr;
+  for (int t = 0; t < NT; ++t) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bv[t][j] = tv ? *reinterpret_cast<const u32x4*>(brow[t] + k0 + 8 * j) : zero4;
-        if (SPLIT) bv2[t][j] = tv ? *reinterpret_cast<const u32x4*>(brow2[t] + k0 + 8 * j) : zero4;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float sc = e8m0_to_f32(sv[r]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 wf = dequant8(wv[r][j], sc);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if (t < ntv) {  // wave-uniform
-            acc[r][t] = mfma16(wf, as_bf16x8(bv[t][j]), acc[r][t]);
-            if (SPLIT) acc[r][t] = mfma16(wf, as_bf16x8(bv2[t][j]), acc[r][t]);
-          }
-        }
-      }
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t off = row_off[t] + k0b + 16u * j;
+      f.b[t][j] = *reinterpret_cast<const u32x4*>(b1 + off);
+      if (SPLIT) f.b2[t][j] = *reinterpret_cast<const u32x4*>(b2 + off);
     }
   }
 }
 
-template <int NT>
-__global__ void __launch_bounds__(256) tkg_gate_up_kernel(
-    const uint16_t* __restrict__ x, int H, int I, const uint8_t* __restrict__ gu_q,
-    const uint8_t* __restrict__ gu_s, const uint16_t* __restrict__ gu_bias,
-    const int32_t* __restrict__ expert_off, const int32_t* __restrict__ active,
-    const int32_t* __restrict__ n_active, const int32_t* __restrict__ slot_tok, ExpertParams p,
-    uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo) {
-  __shared__ f32x4 red[4][2][NT][64];
-  if ((int)blockIdx.y >= *n_active) return;
-  const int e = active[blockIdx.y];
-  const int s0 = expert_off[e], ne = expert_off[e + 1] - s0;
-  const int pair = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const size_t rg_bytes = (size_t)H * 8, rg_sbytes = (size_t)H / 2;
-  const size_t n_rg = (size_t)(2 * I) / 16;
-  const uint8_t* wq = gu_q + ((size_t)e * n_rg + 2 * pair) * rg_bytes;
-  const uint8_t* ws = gu_s + ((size_t)e * n_rg + 2 * pair) * rg_sbytes;
+// No branches around the MFMAs: a branch join would make the compiler copy the
+// accumulators between register files.
+template <int R, int NT, bool SPLIT>
+__device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int c,
+                                          const StreamGeom& g, f32x4 (&acc)[R][NT]) {
+  // chunks at or past nc (the loop rounds up to whole rings) contribute exact zeros
+  const bool ok = (c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float sc = ok ? e8m0_to_f32(f.s[r]) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 wf = dequant8(f.w[r][j], sc);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[r][t] = mfma16(wf, as_bf16x8(f.b[t][j]), acc[r][t]);
+        if (SPLIT) acc[r][t] = mfma16(wf, as_bf16x8(f.b2[t][j]), acc[r][t]);
+      }
+    }
+    // One row group's conversions at a time: registers go to chunks in flight.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// One wave streams an R-row-group tile over all nc K chunks, D chunks in flight.
+// Activation rows are b1 (and, with SPLIT, b2 for the lo parts) plus this lane's
+// byte offset row_off[t] for token tile t (a valid row also for lanes without a token).
+template <int R, int NT, bool SPLIT, int D>
+__device__ __forceinline__ void stream_tile(const StreamGeom& g, const char* b1, const char* b2,
+                                            const uint32_t* row_off, int nc,
+                                            f32x4 (&acc)[R][NT]) {
+  // Every ring slot is refilled right after its MFMAs, unconditionally (past the
+  // end with the last chunk again, a cache hit), and the loop body has no branch:
+  // a load whose issue depends on a branch would make the wait before a chunk's
+  // MFMAs assume the shorter queue and drain the loads of the chunks behind it, and
+  // a branch join around the MFMAs would copy the accumulators.  The loop covers
+  // whole rings; chunks past nc add exact zeros.
+  ChunkFrag<R, NT, SPLIT> f[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    load_chunk(f[d], d < nc ? d : nc - 1, g, b1, b2, row_off);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int c = 0; c < nc; c += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      mma_chunk(f[d], c + d, g, acc);
+      const int cn = c + d + D;
+      load_chunk(f[d], cn < nc ? cn : nc - 1, g, b1, b2, row_off);
+      // Keep program order: the scheduler would otherwise hoist the refills above
+      // the MFMAs and consume them in the same iteration, leaving nothing in flight.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+struct TkgArgs {
+  const uint16_t* x;       // gate_up: tokens [T, H]
+  const uint16_t* h_hi;    // down: activations [slots, I] (hi, lo)
+  const uint16_t* h_lo;
+  const uint8_t* wq;
+  const uint8_t* ws;
+  const uint16_t* bias;    // gate_up [E, 2, I]; down [E, H]; may be null
+  const int32_t* expert_off;
+  const int32_t* active;
+  const int32_t* n_active;
+  const int32_t* slot_tok;
+  uint16_t* out_hi;        // gate_up: h (hi, lo)
+  uint16_t* out_lo;
+  float* y;                // down: [slots, H]
+  int H, I;
+  ExpertParams p;
+};
+
+// One work item = (active expert, R row groups) of the projection GATE_UP selects:
+// stream the item's packed weights against the expert's tokens, then the epilogue.
+// gate_up items hold whole gate/up pairs (R even).
+template <int R, int NT, bool GATE_UP, int D>
+__device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
+  static_assert(!GATE_UP || R % 2 == 0, "gate_up items hold gate/up pairs");
+  constexpr bool SPLIT = !GATE_UP;
+  const int lane = threadIdx.x & 63;
+  const int H = a.H, I = a.I;
+  const int K = GATE_UP ? H : I;
+  const int n_rg = GATE_UP ? (2 * I) / 16 : H / 16;
+  const int nc = (K + 127) / 128;
+  StreamGeom g;
+  g.rg_bytes = (size_t)K * 8;
+  g.rg_sbytes = (size_t)K / 2;
+  g.nfull = K / 128;
+  g.tail_q = (K % 128) / 32;
+  const int ai = item / ipe, ri = item - ai * ipe;
+  // Item metadata is wave-uniform: keep it in scalar registers.
+  const int e = __builtin_amdgcn_readfirstlane(a.active[ai]);
+  const int rg0 = ri * R;
+  g.wq = a.wq + ((size_t)e * n_rg + rg0) * g.rg_bytes;
+  g.ws = a.ws + ((size_t)e * n_rg + rg0) * g.rg_sbytes;
+  g.rv = min(R, n_rg - rg0);
+  const int s0 = __builtin_amdgcn_readfirstlane(a.expert_off[e]);
+  const int ne = __builtin_amdgcn_readfirstlane(a.expert_off[e + 1]) - s0;
+  const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
+                           : reinterpret_cast<const char*>(a.h_hi);
+  const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
   for (int tb = 0; tb < ne; tb += 16 * NT) {
-    const int ntv = min(NT, (ne - tb + 15) / 16);
-    const uint16_t* brow[NT];
+    uint32_t row_off[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int li = tb + 16 * t + (lane & 15);
-      brow[t] = (li < ne) ? x + (size_t)slot_tok[s0 + li] * H : nullptr;
+      const int lr = li < ne ? li : tb;
+      row_off[t] = GATE_UP ? (uint32_t)a.slot_tok[s0 + lr] * (uint32_t)(2 * H)
+                           : (uint32_t)(s0 + lr) * (uint32_t)(2 * I);
     }
-    f32x4 acc[2][NT];
+    f32x4 acc[R][NT];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wave<2, NT, false>(wq, ws, rg_bytes, rg_sbytes, brow, brow, ntv, H, wave, 4, acc);
+    stream_tile<R, NT, SPLIT, D>(g, b1, b2, row_off, nc, acc);
+    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) red[wave][r][t][lane] = acc[r][t];
-    __syncthreads();
-    for (int t = wave; t < ntv; t += 4) {
-      f32x4 g = red[0][0][t][lane], u = red[0][1][t][lane];
-#pragma unroll
-      for (int v = 1; v < 4; ++v) {
-        g += red[v][0][t][lane];
-        u += red[v][1][t][lane];
-      }
+    for (int t = 0; t < NT; ++t) {
       const int li = tb + 16 * t + (lane & 15);
       if (li >= ne) continue;
-      const int col0 = 16 * pair + 4 * (lane >> 4);
       const size_t slot = (size_t)(s0 + li);
-      uint16_t hi[4], lo[4];
+      if (GATE_UP) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float gv = g[i], uv = u[i];
-        if (gu_bias) {
-          gv += bf16_bits_to_f32(gu_bias[(size_t)e * 2 * I + col0 + i]);
-          uv += bf16_bits_to_f32(gu_bias[(size_t)e * 2 * I + I + col0 + i]);
+        for (int pp = 0; pp < R / 2; ++pp) {
+          if (2 * pp >= g.rv) continue;
+          const int col0 = 8 * (rg0 + 2 * pp) + 4 * (lane >> 4);  // 16 * pair index
+          uint16_t hi[4], lo[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float gv = acc[2 * pp][t][i], uv = acc[2 * pp + 1][t][i];
+            if (a.bias) {
+              gv += bf16_bits_to_f32(a.bias[(size_t)e * 2 * I + col0 + i]);
+              uv += bf16_bits_to_f32(a.bias[(size_t)e * 2 * I + I + col0 + i]);
+            }
+            gv = clampf_ref(gv, a.p.gate_lo, a.p.gate_hi);
+            uv = clampf_ref(uv, a.p.up_lo, a.p.up_hi);
+            split_bf16(uv * act_f32(gv, a.p.act), hi[i], lo[i]);
+          }
+          *reinterpret_cast<u16x4*>(a.out_hi + slot * I + col0) = u16x4{hi[0], hi[1], hi[2], hi[3]};
+          *reinterpret_cast<u16x4*>(a.out_lo + slot * I + col0) = u16x4{lo[0], lo[1], lo[2], lo[3]};
         }
-        gv = clampf_ref(gv, p.gate_lo, p.gate_hi);
-        uv = clampf_ref(uv, p.up_lo, p.up_hi);
-        const float h = uv * act_f32(gv, p.act);
-        split_bf16(h, hi[i], lo[i]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r >= g.rv) continue;
+          const int n0 = 16 * (rg0 + r) + 4 * (lane >> 4);
+          f32x4 v = acc[r][t];
+          if (a.bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += bf16_bits_to_f32(a.bias[(size_t)e * H + n0 + i]);
+          }
+          *reinterpret_cast<f32x4*>(a.y + slot * H + n0) = v;
+        }
       }
-      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<u16x4*>(h_hi + slot * I + col0) = u16x4{hi[0], hi[1], hi[2], hi[3]};
-      *reinterpret_cast<u16x4*>(h_lo + slot * I + col0) = u16x4{lo[0], lo[1], lo[2], lo[3]};
     }
-    __syncthreads();
   }
 }
 
-template <int NT>
-__global__ void __launch_bounds__(256) tkg_down_kernel(
-    const uint16_t* __restrict__ h_hi, const uint16_t* __restrict__ h_lo, int H, int I,
-    const uint8_t* __restrict__ dn_q, const uint8_t* __restrict__ dn_s,
-    const uint16_t* __restrict__ dn_bias, const int32_t* __restrict__ expert_off,
-    const int32_t* __restrict__ active, const int32_t* __restrict__ n_active,
-    float* __restrict__ y) {
-  __shared__ f32x4 red[4][2][NT][64];
-  if ((int)blockIdx.y >= *n_active) return;
-  const int e = active[blockIdx.y];
-  const int s0 = expert_off[e], ne = expert_off[e + 1] - s0;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const size_t rg_bytes = (size_t)I * 8, rg_sbytes = (size_t)I / 2;
-  const size_t n_rg = (size_t)H / 16;
-  const int rg0 = 2 * blockIdx.x;
-  const uint8_t* wq = dn_q + ((size_t)e * n_rg + rg0) * rg_bytes;
-  const uint8_t* ws = dn_s + ((size_t)e * n_rg + rg0) * rg_sbytes;
-  for (int tb = 0; tb < ne; tb += 16 * NT) {
-    const int ntv = min(NT, (ne - tb + 15) / 16);
-    const uint16_t* b1[NT];
-    const uint16_t* b2[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int li = tb + 16 * t + (lane & 15);
-      b1[t] = (li < ne) ? h_hi + (size_t)(s0 + li) * I : nullptr;
-      b2[t] = (li < ne) ? h_lo + (size_t)(s0 + li) * I : nullptr;
-    }
-    f32x4 acc[2][NT];
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wave<2, NT, true>(wq, ws, rg_bytes, rg_sbytes, b1, b2, ntv, I, wave, 4, acc);
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) red[wave][r][t][lane] = acc[r][t];
-    __syncthreads();
-    for (int idx = wave; idx < 2 * ntv; idx += 4) {
-      const int r = idx & 1, t = idx >> 1;
-      f32x4 s = red[0][r][t][lane];
-#pragma unroll
-      for (int v = 1; v < 4; ++v) s += red[v][r][t][lane];
-      const int li = tb + 16 * t + (lane & 15);
-      if (li >= ne) continue;
-      const int n0 = 16 * (rg0 + r) + 4 * (lane >> 4);
-      if (dn_bias) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] += bf16_bits_to_f32(dn_bias[(size_t)e * H + n0 + i]);
-      }
-      *reinterpret_cast<f32x4*>(y + (size_t)(s0 + li) * H + n0) = s;
-    }
-    __syncthreads();
-  }
+__host__ __device__ inline int tkg_items_per_expert(int H, int I, bool gate_up, int R) {
+  const int n_rg = gate_up ? (2 * I) / 16 : H / 16;
+  return (n_rg + R - 1) / R;
+}
+
+// Grid dispatch: wave w of workgroup b takes item 4b + w; the grid covers every
+// expert, waves past the active experts' items return at once.
+template <int R, int NT, bool GATE_UP, int D>
+__global__ void __launch_bounds__(256) tkg_stream_kernel(TkgArgs a) {
+  const int ipe = tkg_items_per_expert(a.H, a.I, GATE_UP, R);
+  const int item = blockIdx.x * 4 + wave_id();
+  if (item >= (*a.n_active) * ipe) return;
+  tkg_item<R, NT, GATE_UP, D>(a, item, ipe);
 }
 
 // out[t, n] = bf16(sum_k y[slot(t, k), n] * w(t, k)), k in ascending expert order.
@@ -364,9 +420,108 @@ using namespace mxmoe;
 
 extern "C" size_t mxmoe_moe_tkg_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                                 int top_k) {
-  char* nil = nullptr;
-  return tkg_carve(nil, ~(size_t)0, T, H, I, E, top_k, nullptr);
+  return tkg_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
 }
+
+namespace mxmoe {
+
+static int tkg_check(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
+                     int scale_mode) {
+  MXMOE_REQUIRE(T >= 1 && T <= kTkgMaxT, "moe_tkg: T=%lld out of range [1, %d]", (long long)T,
+                kTkgMaxT);
+  MXMOE_REQUIRE(E >= 1 && E <= kTkgMaxE, "moe_tkg: E=%lld out of range [1, %d]", (long long)E,
+                kTkgMaxE);
+  MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
+                "moe_tkg: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
+  MXMOE_REQUIRE(top_k >= 1 && top_k <= 8, "moe_tkg: top_k=%d out of range [1, 8]", top_k);
+  MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_tkg: unknown activation %d", act);
+  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
+                "moe_tkg: unsupported scale mode %d", scale_mode);
+  return MXMOE_OK;
+}
+
+// route -> gate_up -> down -> combine; ev (may be null) gets 5 marks: before the
+// routing kernel and after each of the four kernels.
+static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
+                        const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                        const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
+                        int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
+                        const float* clamps, int scale_mode, uint16_t* out, const TkgWs& w,
+                        void* const* ev, hipStream_t s) {
+  TkgArgs a = {};
+  a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
+  a.p.gate_hi = clamps ? clamps[1] : INFINITY;
+  a.p.up_lo = clamps ? clamps[2] : -INFINITY;
+  a.p.up_hi = clamps ? clamps[3] : INFINITY;
+  a.p.act = act;
+  a.H = (int)H;
+  a.I = (int)I;
+  a.expert_off = w.expert_off;
+  a.active = w.active;
+  a.n_active = w.n_active;
+  a.slot_tok = w.slot_tok;
+  mark_event(ev, 0, s);
+  hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
+                     top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
+                     w.tok_slot, w.tok_w);
+  mark_event(ev, 1, s);
+  TkgArgs gu = a, dn = a;
+  gu.x = x;
+  gu.wq = gu_q;
+  gu.ws = gu_s;
+  gu.bias = gu_bias;
+  gu.out_hi = w.h_hi;
+  gu.out_lo = w.h_lo;
+  dn.h_hi = w.h_hi;
+  dn.h_lo = w.h_lo;
+  dn.wq = dn_q;
+  dn.ws = dn_s;
+  dn.bias = dn_bias;
+  dn.y = w.y;
+  // One wave per item, four per workgroup; the grid covers every expert (the
+  // active count is known on the device only) and the surplus waves return at once.
+  auto grid = [&](bool gate_up, int R) {
+    return dim3((unsigned)((E * tkg_items_per_expert((int)H, (int)I, gate_up, R) + 3) / 4));
+  };
+  // Token tiles per pass: an expert with more tokens loops over passes.
+  if (T <= 16 || T * top_k <= 8 * E) {
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
+    mark_event(ev, 2, s);
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
+  } else {
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
+    mark_event(ev, 2, s);
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
+  }
+  mark_event(ev, 3, s);
+  hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
+                     dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, out);
+  mark_event(ev, 4, s);
+  return check_launch("moe_tkg");
+}
+
+struct DecodeWs {
+  float* logits;
+  int32_t* idx;
+  float* val;
+  void* tkg;
+  size_t tkg_bytes;
+};
+
+static size_t decode_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
+                           int K, DecodeWs* d) {
+  Carver cv(base, cap);
+  DecodeWs r;
+  r.logits = cv.take<float>(T * E);
+  r.idx = cv.take<int32_t>(T * K);
+  r.val = cv.take<float>(T * K);
+  r.tkg_bytes = tkg_carve(nullptr, ~(size_t)0, T, H, I, E, K, nullptr);
+  r.tkg = cv.take<char>(r.tkg_bytes);
+  if (d) *d = r;
+  return cv.off + 256;
+}
+
+}  // namespace mxmoe
 
 extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
                              const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
@@ -378,54 +533,50 @@ extern "C" int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const f
   clear_error();
   MXMOE_REQUIRE(x && topk_idx && topk_val && gu_q && gu_s && dn_q && dn_s && out && workspace,
                 "moe_tkg: null pointer");
-  MXMOE_REQUIRE(T >= 1 && T <= kTkgMaxT, "moe_tkg: T=%lld out of range [1, %d]", (long long)T,
-                kTkgMaxT);
-  MXMOE_REQUIRE(E >= 1 && E <= kTkgMaxE, "moe_tkg: E=%lld out of range [1, %d]", (long long)E,
-                kTkgMaxE);
-  MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
-                "moe_tkg: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
-  MXMOE_REQUIRE(top_k >= 1 && top_k <= 8, "moe_tkg: top_k=%d out of range [1, 8]", top_k);
-  MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_tkg: unknown activation %d", act);
-  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
-                "moe_tkg: unsupported scale mode %d", scale_mode);
+  int rc = tkg_check(T, H, I, E, top_k, act, scale_mode);
+  if (rc) return rc;
   const size_t need = mxmoe_moe_tkg_workspace_bytes(T, H, I, E, top_k);
   if (workspace_bytes < need)
     return set_error(MXMOE_E_WORKSPACE, "moe_tkg: workspace %zu < %zu", workspace_bytes, need);
   TkgWs w;
   tkg_carve(workspace, workspace_bytes, T, H, I, E, top_k, &w);
-  ExpertParams p;
-  p.gate_lo = clamps ? clamps[0] : -INFINITY;
-  p.gate_hi = clamps ? clamps[1] : INFINITY;
-  p.up_lo = clamps ? clamps[2] : -INFINITY;
-  p.up_hi = clamps ? clamps[3] : INFINITY;
-  p.act = act;
+  return tkg_pipeline(x, topk_idx, topk_val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
+                      top_k, act, clamps, scale_mode, out, w, stage_events, as_stream(stream));
+}
+
+extern "C" size_t mxmoe_moe_decode_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                                   int top_k) {
+  return decode_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
+}
+
+extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
+                                const uint16_t* router_b, int router_act, int act_before_topk,
+                                int renorm, float renorm_eps, const uint8_t* gu_q,
+                                const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
+                                const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T,
+                                int64_t H, int64_t I, int64_t E, int top_k, int act,
+                                const float* clamps, int scale_mode, uint16_t* out,
+                                float* logits_out, void* workspace, size_t workspace_bytes,
+                                void* const* stage_events, void* stream) {
+  clear_error();
+  MXMOE_REQUIRE(x && router_w && gu_q && gu_s && dn_q && dn_s && out && workspace,
+                "moe_decode: null pointer");
+  int rc = tkg_check(T, H, I, E, top_k, act, scale_mode);
+  if (rc) return rc;
+  const size_t need = mxmoe_moe_decode_workspace_bytes(T, H, I, E, top_k);
+  if (workspace_bytes < need)
+    return set_error(MXMOE_E_WORKSPACE, "moe_decode: workspace %zu < %zu", workspace_bytes,
+                     need);
+  DecodeWs d;
+  decode_carve(workspace, workspace_bytes, T, H, I, E, top_k, &d);
+  TkgWs w;
+  tkg_carve(d.tkg, d.tkg_bytes, T, H, I, E, top_k, &w);
   hipStream_t s = as_stream(stream);
-  auto mark = [&](int i) {
-    if (stage_events) hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), s);
-  };
-  mark(0);
-  hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
-                     top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
-                     w.tok_slot, w.tok_w);
-  mark(1);
-  const int64_t maxne = T;  // an expert sees each token at most once
-  const dim3 g1((unsigned)(I / 16), (unsigned)E), g2((unsigned)(H / 32), (unsigned)E);
-#define MXMOE_TKG_LAUNCH(NT)                                                                 \
-  do {                                                                                       \
-    hipLaunchKernelGGL((tkg_gate_up_kernel<NT>), g1, dim3(256), 0, s, x, (int)H, (int)I, gu_q, \
-                       gu_s, gu_bias, w.expert_off, w.active, w.n_active, w.slot_tok, p,     \
-                       w.h_hi, w.h_lo);                                                      \
-    mark(2);                                                                                 \
-    hipLaunchKernelGGL((tkg_down_kernel<NT>), g2, dim3(256), 0, s, w.h_hi, w.h_lo, (int)H,     \
-                       (int)I, dn_q, dn_s, dn_bias, w.expert_off, w.active, w.n_active, w.y); \
-    mark(3);                                                                                 \
-  } while (0)
-  if (maxne <= 16) MXMOE_TKG_LAUNCH(1);
-  else if (maxne <= 32) MXMOE_TKG_LAUNCH(2);
-  else MXMOE_TKG_LAUNCH(4);
-#undef MXMOE_TKG_LAUNCH
-  hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
-                     dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, out);
-  mark(4);
-  return check_launch("moe_tkg");
+  mark_event(stage_events, 0, s);
+  rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
+                  renorm_eps, logits_out ? logits_out : d.logits, nullptr, d.idx, d.val, s);
+  if (rc) return rc;
+  return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
+                      top_k, act, clamps, scale_mode, out, w,
+                      stage_events ? stage_events + 1 : nullptr, s);
 }

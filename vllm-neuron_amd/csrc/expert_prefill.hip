@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   const int lin = xcd * per + min(xcd, rem) + i8;
   const int mt = lin / args.n_ntiles, nt = lin % args.n_ntiles;
   const int m0 = mt * kPM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int q = lane >> 4;
 
   if (tid == 0) s_any = 0;
@@ -358,7 +358,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, &w);
   hipStream_t s = as_stream(stream);
   auto mark = [&](int i) {
-    if (stage_events) hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), s);
+    mark_event(stage_events, i, s);
   };
 
   PrefillArgs a;

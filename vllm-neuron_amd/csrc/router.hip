@@ -15,7 +15,7 @@ __global__ void __launch_bounds__(256) router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, float* __restrict__ logits, int T, int H, int E) {
   __shared__ f32x4 red[4][ET][TT][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, r16 = lane & 15;
   const int t0 = blockIdx.x * 16 * TT, e0 = blockIdx.y * 16 * ET;
   const int nc = (H + 127) / 128;
@@ -213,13 +213,15 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
     for (int k = 0; k < 8; ++k)
       if (k < K) out[k] = out[k] / s;
   }
-  float* arow = aff + (size_t)tok * E;
-  for (int e = lane; e < E; e += 64) {
-    float a = 0.f;
+  if (aff) {
+    float* arow = aff + (size_t)tok * E;
+    for (int e = lane; e < E; e += 64) {
+      float a = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k < K && sel_idx[k] == e) a = out[k];
-    arow[e] = a;
+      for (int k = 0; k < 8; ++k)
+        if (k < K && sel_idx[k] == e) a = out[k];
+      arow[e] = a;
+    }
   }
   if (lane < K) {
     int si = 0;
@@ -266,15 +268,14 @@ using namespace mxmoe;
 
 extern "C" size_t mxmoe_router_workspace_bytes(int64_t, int64_t) { return 0; }
 
-extern "C" int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
-                                 int64_t T, int64_t H, int64_t E, int top_k, int act,
-                                 int act_before_topk, int renorm, float renorm_eps, float* logits, float* affinities, int32_t* topk_idx,
-                                 float* topk_val, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
-  clear_error();
-  MXMOE_REQUIRE(x && w && logits && affinities && topk_idx && topk_val, "router: null pointer");
+namespace mxmoe {
+
+// Shared by mxmoe_router_topk and the fused decode layer; affinities may be null.
+int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64_t T, int64_t H,
+               int64_t E, int top_k, int act, int act_before_topk, int renorm, float renorm_eps,
+               float* logits, float* affinities, int32_t* topk_idx, float* topk_val,
+               hipStream_t s) {
+  MXMOE_REQUIRE(x && w && logits && topk_idx && topk_val, "router: null pointer");
   MXMOE_REQUIRE(T >= 0 && H > 0 && H % 32 == 0, "router: H=%lld must be a positive multiple of 32",
                 (long long)H);
   MXMOE_REQUIRE(E >= 1 && E <= 64 * kMaxEPerLane, "router: E=%lld out of range [1, 1024]",
@@ -283,7 +284,6 @@ extern "C" int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uin
   MXMOE_REQUIRE(act == MXMOE_ROUTER_SOFTMAX || act == MXMOE_ROUTER_SIGMOID,
                 "router: unknown activation %d", act);
   if (T == 0) return MXMOE_OK;
-  hipStream_t s = as_stream(stream);
   if (T >= 1024 && E >= 64) {
     dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
     hipLaunchKernelGGL((router_logits_kernel<4, 4>), grid, dim3(256), 0, s, x, w, bias, logits,
@@ -296,9 +296,24 @@ extern "C" int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uin
   int rc = check_launch("router_logits");
   if (rc) return rc;
   hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, logits,
-                     affinities, topk_idx, topk_val, (int)T, (int)E, top_k, act, act_before_topk ? 1 : 0,
-                     renorm ? 1 : 0, renorm_eps);
+                     affinities, topk_idx, topk_val, (int)T, (int)E, top_k, act,
+                     act_before_topk ? 1 : 0, renorm ? 1 : 0, renorm_eps);
   return check_launch("router_topk");
+}
+
+}  // namespace mxmoe
+
+extern "C" int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                 int64_t T, int64_t H, int64_t E, int top_k, int act,
+                                 int act_before_topk, int renorm, float renorm_eps, float* logits,
+                                 float* affinities, int32_t* topk_idx, float* topk_val,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  clear_error();
+  MXMOE_REQUIRE(affinities, "router: null affinities");
+  return router_run(x, w, bias, T, H, E, top_k, act, act_before_topk, renorm, renorm_eps, logits,
+                    affinities, topk_idx, topk_val, as_stream(stream));
 }
 
 extern "C" int mxmoe_rmsnorm(const uint16_t* x, const float* gamma, int64_t T, int64_t H,

@@ -43,6 +43,8 @@ class MXFP4MoE:
         else:
             self.act = _lib.ACT_SWISH
             self.clamp_args = (None, swiglu_limit, -swiglu_limit + 1, swiglu_limit + 1)
+        self._clamps = _lib.clamps_array(*self.clamp_args)
+        self._ws = {}
 
     @property
     def E(self) -> int:
@@ -68,9 +70,27 @@ class MXFP4MoE:
                        up_clamp_upper_limit=u_hi, up_clamp_lower_limit=u_lo,
                        output_dtype=output_dtype, stage_events=stage_events)
 
-    def decode(self, x: torch.Tensor, stage_events=None):
-        _, _, idx, val = self.route(x)
+    def decode(self, x: torch.Tensor, stage_events=None, logits_out=None):
+        """Router + experts in one library call (mxmoe_moe_decode).  The workspace is
+        cached per token count, so calls of one layer object belong on one stream."""
         w = self.w
-        return moe_tkg_raw(x, idx, val, w.gu_q, w.gu_s, w.dn_q, w.dn_s, w.gu_bias, w.dn_bias,
-                           self.act, _lib.clamps_array(*self.clamp_args), _lib.SCALE_POST,
-                           stage_events)
+        T, H = x.shape
+        dev = _lib.require_cuda(x, w.gu_q)
+        if x.dtype != torch.bfloat16 or H != w.H:
+            raise ValueError(f"expected bf16 [T, {w.H}] hidden states")
+        L = _lib.lib()
+        ws = self._ws.get(T)
+        if ws is None:
+            ws = _lib.workspace(L.mxmoe_moe_decode_workspace_bytes(T, H, w.I, w.E, self.top_k), dev)
+            self._ws[T] = ws
+        x = x.contiguous()
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        rc = L.mxmoe_moe_decode(
+            x.data_ptr(), self.router_w.data_ptr(), _lib.ptr(self.router_b), _lib.ROUTER_SOFTMAX,
+            0, 0, 0.0, w.gu_q.data_ptr(), w.gu_s.data_ptr(), w.dn_q.data_ptr(),
+            w.dn_s.data_ptr(), _lib.ptr(w.gu_bias), _lib.ptr(w.dn_bias), T, H, w.I, w.E,
+            self.top_k, self.act, self._clamps, _lib.SCALE_POST, out.data_ptr(),
+            _lib.ptr(logits_out), ws.data_ptr(), ws.numel(), _lib.event_array(stage_events),
+            _lib.stream_handle(dev))
+        _lib.check(rc, "mxmoe_moe_decode")
+        return out
