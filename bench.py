@@ -99,6 +99,18 @@ def gate_up_bytes_per_expert(H, I, biases):
     return 2 * I * H // 2 + 2 * I * H // 32 + (2 * I * 2 if biases else 0)
 
 
+def measured_traffic(workload, decode_T):
+    """HBM bytes per launch of the decode gate_up kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) for this workload, else None."""
+    path = ROOT / "profiles" / f"decode_traffic_{workload}.json"
+    if not path.exists():
+        return None, None
+    d = json.loads(path.read_text())
+    if d.get("decode_tokens") != decode_T:
+        return None, None
+    return d["traffic_bytes"], d["source"]
+
+
 def cpu_baseline(wl, decode_T, prefill_T):
     """Time the CPU oracle on a bounded sample; returns dicts for decode and prefill."""
     import torch
@@ -111,34 +123,38 @@ def cpu_baseline(wl, decode_T, prefill_T):
     from oracle.layer import RefLayer
 
     E, K, H, I, limit, biases, _, _ = WORKLOADS[wl]
-    cores = len(os.sched_getaffinity(0))
+    cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
-    e_s = 8
+    e_s = min(E, 16)
     shape = synthetic.MoEShape(wl + "-sample", E, min(K, e_s), H, I, limit, biases)
     ref = RefLayer(synthetic.layer_tensors(shape, 5, E=e_s))
+
+    def timed(fn, budget_s):
+        fn()  # warm-up
+        ts = []
+        while len(ts) < 3 or sum(ts) < budget_s:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2], len(ts)
+
     res = {}
     x = synthetic.tokens(5, decode_T, H)
-    ref.decode(x)  # warm-up
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        ref.decode(x)
-        ts.append(time.perf_counter() - t0)
-    t = sorted(ts)[1] * E / e_s
+    t, n = timed(lambda: ref.decode(x), 8.0)
+    t *= E / e_s
     res["decode"] = {"value": decode_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
                      "sample": f"dense all-expert fp32 decode (reference moe_block_tkg CPU flow) "
-                               f"of {decode_T} tokens over {e_s} of {E} experts, median of 3, "
-                               f"time scaled x{E // e_s} (linear in experts)"}
-    t_s = min(prefill_T, 256)
+                               f"of {decode_T} tokens over {e_s} of {E} experts, median of {n} "
+                               f"reps (about 8 s), time scaled x{E / e_s:g} (linear in experts)"}
+    t_s = min(prefill_T, 512)
     xp = synthetic.tokens(6, t_s, H)
-    ref.prefill(xp)
-    t0 = time.perf_counter()
-    ref.prefill(xp)
-    t = (time.perf_counter() - t0) * (E / e_s) * (prefill_T / t_s)
+    t, n = timed(lambda: ref.prefill(xp), 8.0)
+    t *= (E / e_s) * (prefill_T / t_s)
     res["prefill"] = {"value": prefill_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
                       "sample": f"dense all-expert bf16 prefill (reference _torch_moe_impl CPU "
-                                f"flow) of {t_s} tokens over {e_s} of {E} experts, 1 rep, time "
-                                f"scaled x{E // e_s} (experts) x{prefill_T / t_s:g} (tokens)"}
+                                f"flow) of {t_s} tokens over {e_s} of {E} experts, median of {n} "
+                                f"reps (about 8 s), time scaled x{E / e_s:g} (experts) "
+                                f"x{prefill_T / t_s:g} (tokens)"}
     return res
 
 
@@ -249,10 +265,11 @@ def main():
         "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
     }
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "kernel": "tkg_gate_up_kernel", "achieved": gu_gbs,
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gu_gbs / HBM_PEAK_GBS,
-                "traffic": None, "algorithmic_bytes_per_launch": gu_bytes,
-                "avg_launch_ms": gu_ms}
+    traffic, traffic_src = measured_traffic(args.workload, dT)
+    roofline = {"bound": "hbm", "kernel": "tkg_stream_kernel<4, 1, true, 2> (gate_up)",
+                "achieved": gu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": gu_gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                "algorithmic_bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
 
     # ---------------- prefill
     prefill = None
