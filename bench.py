@@ -79,9 +79,9 @@ def make_layer(E, K, H, I, limit, biases, dev, gen):
         return (torch.randn(shape, device=dev, generator=gen) * std).to(torch.bfloat16)
 
     gu_q = rbytes(E, 2 * I // 16, 8 * H)
-    gu_s = rbytes(E, 2 * I // 16, H // 2, lo=120, hi=131)
+    gu_s = rbytes(E, (2 * I + 63) // 64, 2 * H, lo=120, hi=131)
     dn_q = rbytes(E, H // 16, 8 * I)
-    dn_s = rbytes(E, H // 16, I // 2, lo=120, hi=131)
+    dn_s = rbytes(E, (H + 63) // 64, 2 * I, lo=120, hi=131)
     gub = rnorm(E, 2, I) if biases else None
     if gub is not None and limit is not None:
         gub[:, 1] += 1.0  # the loader pre-adds +1 to the up bias (GPT-OSS)

@@ -16,7 +16,9 @@
  *   packed     weights in the row-group/chunk tile layout produced at load time
  *              by vllm_neuron_amd.weights.pack_mxfp4 (rows grouped by 16, K cut
  *              into 128-element chunks; see vllm-neuron_amd/csrc/common.h).
- *              A [N, K] matrix takes N*K/2 data bytes and N*K/32 scale bytes.
+ *              Scales keep row groups four at a time (one 32-bit word per lane
+ *              and chunk covers a quad).  A [N, K] matrix takes N*K/2 data
+ *              bytes and ceil(N/64)*2K scale bytes.
  *              Fused gate_up matrices alternate 16-row groups of gate and up
  *              rows: [gate 0..15, up 0..15, gate 16..31, up 16..31, ...].
  *   clamps     float[4] = {gate_lo, gate_hi, up_lo, up_hi}; pass -INFINITY /

@@ -94,20 +94,32 @@ def test_pack_unpack_roundtrip_and_layout():
     from vllm_neuron_amd.weights import pack_mxfp4, unpack_mxfp4
 
     g = torch.Generator().manual_seed(0)
-    for N, K in ((16, 32), (32, 96), (48, 128), (16, 2880), (32, 320)):
+    for N, K in ((16, 32), (32, 96), (48, 128), (16, 2880), (32, 320), (64, 160), (80, 2880)):
         blocks = torch.randint(0, 256, (2, N, K // 32, 16), generator=g, dtype=torch.uint8)
         scales = torch.randint(0, 256, (2, N, K // 32), generator=g, dtype=torch.uint8)
         d, s = pack_mxfp4(blocks, scales)
-        assert d.shape == (2, N // 16, 8 * K) and s.shape == (2, N // 16, K // 2)
+        assert d.shape == (2, N // 16, 8 * K) and s.shape == (2, (N + 63) // 64, 2 * K)
         b2, s2 = unpack_mxfp4(d, s)
         assert torch.equal(b2, blocks) and torch.equal(s2, scales)
-        # spot-check the documented addressing: lane l of chunk c of row group r
-        for (r, c, l) in ((0, 0, 0), (0, 0, 17), (N // 16 - 1, (K - 1) // 128, 5)):
-            row, kb = 16 * r + l % 16, 4 * c + l // 16
-            if kb >= K // 32:
-                continue
-            assert torch.equal(d[1, r, c * 1024 + l * 16:c * 1024 + l * 16 + 16], blocks[1, row, kb])
-            assert s[1, r, c * 64 + l] == scales[1, row, kb]
+        # the documented addressing, for every (row group, chunk, lane): data of lane l
+        # of chunk c of row group g at g*8K + c*1024 + 16l, scale at q*2K + c*256 + 4l + r
+        # (q, r = divmod(g, 4)); lanes past K in a partial last chunk hold nothing
+        for g_ in range(N // 16):
+            q, r = divmod(g_, 4)
+            for c in range((K + 127) // 128):
+                for l in range(64):
+                    row, kb = 16 * g_ + l % 16, 4 * c + l // 16
+                    if kb >= K // 32:
+                        continue
+                    o = c * 1024 + l * 16
+                    assert torch.equal(d[1, g_, o:o + 16], blocks[1, row, kb])
+                    assert s[1, q, c * 256 + 4 * l + r] == scales[1, row, kb]
+        # padding of a partial last quad is zero
+        nrg = N // 16
+        if nrg % 4:
+            for g_ in range(nrg, 4 * ((nrg + 3) // 4)):
+                q, r = divmod(g_, 4)
+                assert int(s[:, q].reshape(2, -1, 4)[..., r].sum()) == 0
 
 
 def test_mxfp4_linear_oracle_is_fp32_matmul_of_dequant():

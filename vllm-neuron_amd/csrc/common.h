@@ -9,8 +9,11 @@
 //   * inside a chunk, lane l of a wave owns row rg*16 + (l % 16) and K-block
 //     4*c + l/16: its 16 bytes are stored at  rg*(K*8) + c*1024 + l*16, so a wave
 //     reads one chunk of one row group with a single coalesced 1 KiB load;
-//   * its E8M0 scale is stored at rg*(K/2) + c*64 + l.
-// A row group therefore occupies K*8 data bytes and K/2 scale bytes.
+//   * scales keep row groups four at a time (quad q = rg / 4, r = rg % 4): the
+//     E8M0 byte of that lane is at q*(2K) + c*256 + 4*l + r, so one 32-bit load
+//     per lane gives the scales of a quad's four row groups; a partial last quad
+//     is padded with zero bytes.
+// A row group therefore occupies K*8 data bytes and a quad 2K scale bytes.
 //
 // MFMA operand convention (v_mfma_f32_16x16x32_bf16): A lane l holds row l%16,
 // B lane l holds column l%16, and both hold 8 K-values chosen by (l/16, element).

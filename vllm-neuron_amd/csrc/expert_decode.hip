@@ -135,21 +135,23 @@ __device__ __forceinline__ float act_f32(float g, int act) {
   return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
 }
 
-// Registers of one K chunk of a streamed tile: R weight row groups (16 B + one
-// scale byte per lane each) and NT token tiles of activations (4 x 16 B per lane;
-// with SPLIT a second (lo) copy).
+// Registers of one K chunk of a streamed tile: R = 4 weight row groups (16 B per
+// lane each), their four scale bytes (one 32-bit word per lane: the packed scales
+// keep a quad of row groups together) and NT token tiles of activations (4 x 16 B
+// per lane; with SPLIT a second (lo) copy).
 template <int R, int NT, bool SPLIT>
 struct ChunkFrag {
+  static_assert(R == 4, "a streamed tile is one quad of row groups");
   u32x4 w[R];
-  uint32_t s[R];
+  uint32_t s;
   u32x4 b[NT][4];
   u32x4 b2[SPLIT ? NT : 1][4];
 };
 
 struct StreamGeom {
   const uint8_t* wq;  // first row group of the tile
-  const uint8_t* ws;
-  size_t rg_bytes, rg_sbytes;
+  const uint8_t* ws;  // the tile's quad of scales
+  size_t rg_bytes;
   int rv;             // valid row groups in the tile (<= R)
   int nfull, tail_q;  // full 128-wide chunks, 32-blocks in the partial last chunk
 };
@@ -172,12 +174,11 @@ __device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, co
   for (int r = 0; r < R; ++r) {
     const int rr = r < g.rv ? r : g.rv - 1;
     const uint8_t* wb = g.wq + rr * g.rg_bytes + (size_t)c * 1024;  // wave-uniform
-    const uint8_t* sb = g.ws + rr * g.rg_sbytes + (size_t)c * 64;
     // Weights are read once per step: non-temporal, so they do not evict the
     // activations and scales that neighbouring waves re-read from the caches.
     f.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + lo * 16u));
-    f.s[r] = sb[lo];
   }
+  f.s = *reinterpret_cast<const uint32_t*>(g.ws + (size_t)c * 256 + lo * 4u);
   const uint32_t k0b = ok ? (uint32_t)(c * 128 + q * 32) * 2u : 0u;  // byte offset in a row
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -199,7 +200,7 @@ __device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int 
   const bool ok = (c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float sc = ok ? e8m0_to_f32(f.s[r]) : 0.0f;
+    const float sc = ok ? e8m0_to_f32((f.s >> (8 * r)) & 0xffu) : 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 wf = dequant8(f.w[r][j], sc);
@@ -278,7 +279,6 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   const int nc = (K + 127) / 128;
   StreamGeom g;
   g.rg_bytes = (size_t)K * 8;
-  g.rg_sbytes = (size_t)K / 2;
   g.nfull = K / 128;
   g.tail_q = (K % 128) / 32;
   const int ai = item / ipe, ri = item - ai * ipe;
@@ -286,7 +286,7 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   const int e = __builtin_amdgcn_readfirstlane(a.active[ai]);
   const int rg0 = ri * R;
   g.wq = a.wq + ((size_t)e * n_rg + rg0) * g.rg_bytes;
-  g.ws = a.ws + ((size_t)e * n_rg + rg0) * g.rg_sbytes;
+  g.ws = a.ws + ((size_t)e * ((n_rg + 3) / 4) + rg0 / 4) * (size_t)(2 * K);
   g.rv = min(R, n_rg - rg0);
   const int s0 = __builtin_amdgcn_readfirstlane(a.expert_off[e]);
   const int ne = __builtin_amdgcn_readfirstlane(a.expert_off[e + 1]) - s0;

@@ -96,12 +96,12 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
 
   const int e = args.b2e ? args.b2e[m0 / args.B] : 0;
   const int K = args.K;
-  const size_t rg_bytes = (size_t)K * 8, rg_sbytes = (size_t)K / 2;
+  const size_t rg_bytes = (size_t)K * 8, q_sbytes = (size_t)K * 2;
   const int n_rg_total = args.N_rows / 16;
-  const int rg0 = nt * kPRG;
+  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds 4 scale quads
   const int rg_valid = min(kPRG, n_rg_total - rg0);
   const uint8_t* wq = args.wq + ((size_t)e * n_rg_total + rg0) * rg_bytes;
-  const uint8_t* ws = args.ws + ((size_t)e * n_rg_total + rg0) * rg_sbytes;
+  const uint8_t* ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rg0 / 4) * q_sbytes;
   const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
 
   // ---- global -> register staging assignment
@@ -119,8 +119,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   // B: 2 pieces of 16 B: rg = (tid + 512 i) / 64, l16 = tid % 64
   const int b_l = tid & 63;
   const int b_rg0 = tid >> 6;  // + 8 i
-  // S: threads < 256, 4 bytes: rg = tid / 16, b4 = tid % 16
-  const int s_rg = tid >> 4, s_b4 = tid & 15;
+  // S: threads < 256, one word (a quad's 4 scale bytes) of lane s_l of quad s_q
+  const int s_q = tid >> 6, s_l = tid & 63;
 
   u32x4 ra[4], rbw[2];
   uint32_t rs = 0;
@@ -141,8 +141,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
                   : zero4;
     }
     if (tid < 256) {
-      const bool ok = s_rg < rg_valid && (c < nfull || (s_b4 >> 2) < tail_q);
-      rs = ok ? *reinterpret_cast<const uint32_t*>(ws + s_rg * rg_sbytes + (size_t)c * 64 + s_b4 * 4)
+      const bool ok = 4 * s_q < rg_valid && (c < nfull || (s_l >> 4) < tail_q);
+      rs = ok ? *reinterpret_cast<const uint32_t*>(ws + s_q * q_sbytes + (size_t)c * 256 + s_l * 4)
               : 0u;
     }
   };
@@ -153,7 +153,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       *reinterpret_cast<u32x4*>(&sb[st][(b_rg0 + 8 * i) * 1024 + b_l * 16]) = rbw[i];
-    if (tid < 256) *reinterpret_cast<uint32_t*>(&ss[st][s_rg * 64 + s_b4 * 4]) = rs;
+    if (tid < 256) *reinterpret_cast<uint32_t*>(&ss[st][s_q * 256 + s_l * 4]) = rs;
   };
 
   const int wm = wave & 1, wn = wave >> 1;
@@ -178,10 +178,11 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     if (active) {
       u32x4 wv[4];
       float sc[4];
+      const uint32_t s4 = *reinterpret_cast<const uint32_t*>(&ss[st][wn * 256 + lane * 4]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         wv[r] = *reinterpret_cast<const u32x4*>(&sb[st][(4 * wn + r) * 1024 + lane * 16]);
-        sc[r] = e8m0_to_f32(ss[st][(4 * wn + r) * 64 + lane]);
+        sc[r] = e8m0_to_f32((s4 >> (8 * r)) & 0xffu);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {

@@ -43,8 +43,8 @@ def expert_shapes(gu_q: Tensor, gu_s: Tensor, dn_q: Tensor, dn_s: Tensor):
     E = gu_q.shape[0]
     H = gu_q.shape[2] // 8
     I = gu_q.shape[1] * 16 // 2
-    exp = {"gu_s": (E, 2 * I // 16, H // 2), "dn_q": (E, H // 16, 8 * I),
-           "dn_s": (E, H // 16, I // 2)}
+    exp = {"gu_s": (E, (2 * I + 63) // 64, 2 * H), "dn_q": (E, H // 16, 8 * I),
+           "dn_s": (E, (H + 63) // 64, 2 * I)}
     got = {"gu_s": tuple(gu_s.shape), "dn_q": tuple(dn_q.shape), "dn_s": tuple(dn_s.shape)}
     for k in exp:
         if exp[k] != got[k]:

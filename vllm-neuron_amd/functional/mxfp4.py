@@ -33,13 +33,13 @@ def dequantize_mxfp4_to_bf16(blocks: Tensor, scales: Tensor, _hw_probe: bool = F
 
 
 def mxfp4_linear(x: Tensor, w_packed: Tensor, w_scale: Tensor) -> Tensor:
-    """x bf16 [M, K]; W packed [N/16, 8K] + [N/16, K/2] -> y bf16 [M, N]."""
+    """x bf16 [M, K]; W packed [N/16, 8K] + [ceil(N/64), 2K] -> y bf16 [M, N]."""
     dev = _lib.require_cuda(x, w_packed, w_scale)
     if x.dtype != torch.bfloat16:
         raise NotImplementedError("x must be bfloat16")
     M, K = x.shape
     N = w_packed.shape[0] * 16
-    if w_packed.shape[1] != 8 * K or tuple(w_scale.shape) != (N // 16, K // 2):
+    if w_packed.shape[1] != 8 * K or tuple(w_scale.shape) != ((N + 63) // 64, 2 * K):
         raise ValueError("packed weight shape does not match x")
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     rc = _lib.lib().mxmoe_linear(x.contiguous().data_ptr(), M, w_packed.contiguous().data_ptr(),

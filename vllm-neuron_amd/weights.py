@@ -14,7 +14,10 @@ Packed layout of one [N, K] matrix (rows grouped by 16, K in 128-element chunks)
   data  [N/16, 8K] bytes: chunk c of row group g at g*8K + c*1024; inside it the
         16 bytes of lane l are row 16g + l%16, K-block 4c + l//16 (a partial last
         chunk keeps only its lanes l < 16 * blocks_in_chunk);
-  scale [N/16, K/2] bytes: the E8M0 byte of that (row, K-block) at g*K/2 + c*64 + l.
+  scale [ceil(N/64), 2K] bytes, row groups taken four at a time ("quads"): the E8M0
+        byte of row group g = 4q + r, chunk c, lane l is at q*2K + c*256 + 4l + r, so
+        one 32-bit word per lane holds the scales of a quad's four row groups (a
+        partial last quad is padded with zero bytes).
 Fused gate_up matrices alternate 16-row groups of gate and up rows.
 
 Every function here is a pure layout transform (torch views/permutes) that runs on
@@ -30,30 +33,35 @@ import torch
 
 
 def _pack_2d(blocks: torch.Tensor, scales: torch.Tensor):
-    """blocks [L, N, G, 16], scales [L, N, G] -> data [L, N/16, 256G], scale [L, N/16, 16G]."""
+    """blocks [L, N, G, 16], scales [L, N, G] -> data [L, N/16, 256G], scale [L, NQ, 64G]
+    with NQ = ceil(N/64)."""
     L, N, G, _ = blocks.shape
     if N % 16:
         raise ValueError(f"row count {N} must be a multiple of 16")
     nrg, nfull, tq = N // 16, G // 4, G % 4
+    nq = (nrg + 3) // 4
     b = blocks.reshape(L, nrg, 16, G, 16)
-    s = scales.reshape(L, nrg, 16, G)
+    s = scales.reshape(L, N, G)
+    if nq * 64 != N:
+        s = torch.cat([s, s.new_zeros(L, nq * 64 - N, G)], 1)
+    s = s.reshape(L, nq, 4, 16, G)  # quad, r, row, block
     parts_d, parts_s = [], []
     if nfull:
         bf = b[:, :, :, :4 * nfull, :].reshape(L, nrg, 16, nfull, 4, 16)
         parts_d.append(bf.permute(0, 1, 3, 4, 2, 5).reshape(L, nrg, nfull * 1024))
-        sf = s[:, :, :, :4 * nfull].reshape(L, nrg, 16, nfull, 4)
-        parts_s.append(sf.permute(0, 1, 3, 4, 2).reshape(L, nrg, nfull * 64))
+        sf = s[..., :4 * nfull].reshape(L, nq, 4, 16, nfull, 4)  # quad, r, row, c, kq
+        parts_s.append(sf.permute(0, 1, 4, 5, 3, 2).reshape(L, nq, nfull * 256))
     if tq:
         bt = b[:, :, :, 4 * nfull:, :]  # [L, rg, r, tq, byte]
         parts_d.append(bt.permute(0, 1, 3, 2, 4).reshape(L, nrg, tq * 256))
-        st = s[:, :, :, 4 * nfull:]
-        parts_s.append(st.permute(0, 1, 3, 2).reshape(L, nrg, tq * 16))
+        st = s[..., 4 * nfull:]  # quad, r, row, kq
+        parts_s.append(st.permute(0, 1, 4, 3, 2).reshape(L, nq, tq * 64))
     return torch.cat(parts_d, -1).contiguous(), torch.cat(parts_s, -1).contiguous()
 
 
 def pack_mxfp4(blocks: torch.Tensor, scales: torch.Tensor):
     """OCP blocks [..., N, K/32, 16] + scales [..., N, K/32] -> packed (data, scale)
-    with shapes [..., N/16, 8K] and [..., N/16, K/2]."""
+    with shapes [..., N/16, 8K] and [..., ceil(N/64), 2K]."""
     if blocks.dtype != torch.uint8 or scales.dtype != torch.uint8:
         raise TypeError("MXFP4 blocks and scales must be uint8")
     lead = blocks.shape[:-3]
@@ -61,31 +69,39 @@ def pack_mxfp4(blocks: torch.Tensor, scales: torch.Tensor):
     if blocks.shape[-1] != 16 or tuple(scales.shape) != tuple(blocks.shape[:-1]):
         raise ValueError("expected blocks [..., N, G, 16] and scales [..., N, G]")
     d, s = _pack_2d(blocks.reshape(-1, N, G, 16), scales.reshape(-1, N, G))
-    return d.reshape(*lead, N // 16, G * 256), s.reshape(*lead, N // 16, G * 16)
+    return d.reshape(*lead, N // 16, G * 256), s.reshape(*lead, (N + 63) // 64, G * 64)
+
+
+def packed_scale_shape(N: int, K: int):
+    """Trailing shape of the packed scale tensor of an [N, K] matrix."""
+    return ((N + 63) // 64, 2 * K)
 
 
 def unpack_mxfp4(data: torch.Tensor, scale: torch.Tensor):
-    """Inverse of pack_mxfp4: packed [..., N/16, 8K] + [..., N/16, K/2] -> OCP blocks/scales."""
+    """Inverse of pack_mxfp4: packed [..., N/16, 8K] + [..., ceil(N/64), 2K] ->
+    OCP blocks [..., N, K/32, 16] and scales [..., N, K/32]."""
     lead = data.shape[:-2]
     nrg, nbytes = data.shape[-2], data.shape[-1]
     G = nbytes // 256
     nfull, tq = G // 4, G % 4
+    nq = (nrg + 3) // 4
     d = data.reshape(-1, nrg, nbytes)
-    s = scale.reshape(-1, nrg, G * 16)
+    s = scale.reshape(-1, nq, G * 64)
     L = d.shape[0]
     outs_b, outs_s = [], []
     if nfull:
         bf = d[:, :, :nfull * 1024].reshape(L, nrg, nfull, 4, 16, 16)  # rg, c, q, r, byte
         outs_b.append(bf.permute(0, 1, 4, 2, 3, 5).reshape(L, nrg, 16, nfull * 4, 16))
-        sf = s[:, :, :nfull * 64].reshape(L, nrg, nfull, 4, 16)
-        outs_s.append(sf.permute(0, 1, 4, 2, 3).reshape(L, nrg, 16, nfull * 4))
+        sf = s[:, :, :nfull * 256].reshape(L, nq, nfull, 4, 16, 4)  # quad, c, kq, row, r
+        outs_s.append(sf.permute(0, 1, 5, 4, 2, 3).reshape(L, nq, 4, 16, nfull * 4))
     if tq:
         bt = d[:, :, nfull * 1024:].reshape(L, nrg, tq, 16, 16)  # rg, tq, r, byte
         outs_b.append(bt.permute(0, 1, 3, 2, 4))
-        st = s[:, :, nfull * 64:].reshape(L, nrg, tq, 16)
-        outs_s.append(st.permute(0, 1, 3, 2))
+        st = s[:, :, nfull * 256:].reshape(L, nq, tq, 16, 4)  # quad, kq, row, r
+        outs_s.append(st.permute(0, 1, 4, 3, 2))
     b = torch.cat(outs_b, 3).reshape(*lead, nrg * 16, G, 16)
-    sc = torch.cat(outs_s, 3).reshape(*lead, nrg * 16, G)
+    sc = torch.cat(outs_s, 4).reshape(-1, nq * 64, G)[:, :nrg * 16]
+    sc = sc.reshape(*lead, nrg * 16, G)
     return b.contiguous(), sc.contiguous()
 
 
@@ -118,8 +134,8 @@ def gate_up_bias_from_checkpoint(bias: torch.Tensor, up_offset: float = 1.0) -> 
 class MXFP4Experts:
     """Packed expert weights of one MoE layer (all tensors on one device).
 
-    gu_q [E, 2I/16, 8H], gu_s [E, 2I/16, H/2]  fused gate_up (row groups alternate gate/up)
-    dn_q [E, H/16, 8I],  dn_s [E, H/16, I/2]   down projection
+    gu_q [E, 2I/16, 8H], gu_s [E, ceil(2I/64), 2H]  fused gate_up (row groups alternate gate/up)
+    dn_q [E, H/16, 8I],  dn_s [E, ceil(H/64), 2I]   down projection
     gu_bias [E, 2, I] bf16 (up half already holds +1 for GPT-OSS) or None
     dn_bias [E, H] bf16 or None
     """
