@@ -41,6 +41,21 @@ def routing_agreement(layer, ref, x, dev):
     return aff_r, bad
 
 
+def routing_from_logits(logits_g, ref, x):
+    """Like routing_agreement, for logits a fused GPU call returned (logits_out)."""
+    aff_r, logits_r = ref.route(x)
+    logits_g = logits_g.cpu()
+    assert torch.allclose(logits_g, logits_r, rtol=1e-5, atol=1e-5)
+    k = ref.K
+    sel_g = torch.zeros_like(logits_g, dtype=torch.bool)
+    sel_g.scatter_(1, torch.topk(logits_g, k, dim=1).indices, True)
+    bad = (sel_g != (aff_r != 0)).any(1)
+    for t in torch.nonzero(bad).flatten().tolist():
+        srt = torch.sort(logits_r[t], descending=True).values
+        assert (srt[k - 1] - srt[k]).abs() < 1e-5 * max(1.0, srt[0].abs().item())
+    return aff_r, bad
+
+
 def check_close(got, want, skip_rows=None, label=""):
     got = got.double()
     want = want.double()

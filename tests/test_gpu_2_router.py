@@ -41,7 +41,7 @@ def compare_routing(aff_g, logits_g, aff_r, logits_r, k):
 
 @pytest.mark.parametrize("T,E,k,H", [(1, 32, 4, 2880), (64, 128, 4, 2880), (4096, 32, 4, 2880),
                                      (4096, 128, 4, 2880), (128, 256, 8, 7168), (17, 8, 2, 64),
-                                     (1000, 1024, 8, 256)])
+                                     (64, 512, 4, 256), (33, 300, 8, 128), (1000, 1024, 8, 256)])
 def test_router_softmax(dev, T, E, k, H):
     from vllm_neuron_amd import functional as NF
 
@@ -81,7 +81,9 @@ def test_rmsnorm_router_block_tkg_front_end(dev):
     xn_r, logits_r, top_r, idx_r = obt.rmsnorm_router(x, gamma, w.T, None, 1e-5, k, "SOFTMAX",
                                                       False, True, hidden_actual=2800)
     d = (xn_g.float() - xn_r.float()).abs()
-    assert torch.all(d <= xn_r.float().abs() * 2.0 ** -8), d.max()  # <= 1 bf16 ulp
+    # one bf16 ulp of each reference value (the fp32 variance sums in another order)
+    ulp = torch.ldexp(torch.ones_like(d), torch.frexp(xn_r.float()).exponent - 8)
+    assert torch.all(d <= ulp), d.max()
     assert (d == 0).float().mean() > 0.99
     # router stage on the reference's normalized rows, with renorm (+1e-20)
     _, logits_g, idx_g, val_g = router_topk_raw(xn_r.to(dev), w.to(dev), k, None, 0, False, True,

@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from moe_helpers import build, check_close, routing_agreement
+from moe_helpers import build, check_close, routing_from_logits
 
 pytestmark = pytest.mark.gpu
 
@@ -21,10 +21,73 @@ def test_decode_gptoss20b(dev, gptoss20, T):
 
     ref, layer, _ = gptoss20
     x = synthetic.tokens(21, T, ref.H)
-    aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.decode(x.to(dev)).cpu()
+    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, f"decode 20b T={T}")
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_decode_repeated_calls_and_graph_replays(dev, gptoss20, T):
+    """Consecutive calls on one cached workspace, and replays of a captured graph with
+    eager work in between, give the same bits as the first eager call."""
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = gptoss20
+    x = synthetic.tokens(31, T, ref.H).to(dev)
+    first = layer.decode(x)
+    for _ in range(3):
+        assert torch.equal(layer.decode(x), first)
+    x2 = synthetic.tokens(32, T, ref.H).to(dev)
+    other = layer.decode(x2)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            out = layer.decode(x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), f"replay {i}"
+        assert torch.equal(layer.decode(x2), other)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("E,k,T", [(300, 8, 37), (512, 4, 128)])
+def test_decode_wide_expert_counts(dev, E, k, T):
+    """Expert counts that are not multiples of 64 and the widest rows of the decode
+    front end's top-k (up to 8 logits per lane)."""
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape(f"wide{E}", E, k, 256, 256)
+    ref, layer, _ = build(shape, 40 + E, dev, exp=(118, 122))
+    x = synthetic.tokens(41, T, ref.H)
+    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, f"decode E={E} k={k} T={T}")
+
+
+@pytest.mark.parametrize("T", [200, 256])
+def test_decode_large_batch(dev, gptoss20, T):
+    """Batches past the fused front end (standalone router + routing kernels) and with
+    more than 8 routed tokens per expert on average (two token tiles per pass)."""
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = gptoss20
+    x = synthetic.tokens(33, T, ref.H)
+    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
+    rows = torch.arange(0, T, 7)
+    want = ref.decode_routed(x[rows], aff[rows])
+    check_close(got[rows], want, ties[rows], f"decode 20b T={T} sample")
 
 
 def test_decode_unsaturated_weights(dev):
@@ -32,8 +95,9 @@ def test_decode_unsaturated_weights(dev):
 
     ref, layer, _ = build(synthetic.GPT_OSS_20B, 2, dev, E=16, exp=(116, 120))
     x = synthetic.tokens(22, 40, ref.H)
-    aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.decode(x.to(dev)).cpu()
+    logits = torch.empty(40, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode unsaturated")
 
@@ -55,8 +119,9 @@ def test_decode_plain_swiglu_fine_grained(dev):
 
     ref, layer, _ = build(synthetic.FINE_GRAINED, 4, dev, E=32)
     x = synthetic.tokens(24, 8, ref.H)
-    aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.decode(x.to(dev)).cpu()
+    logits = torch.empty(8, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode plain swiglu")
 
@@ -129,8 +194,9 @@ def test_decode_gptoss120b_t64_sample(dev):
 
     ref, layer, _ = build(synthetic.GPT_OSS_120B, 7, dev)
     x = synthetic.tokens(27, 64, ref.H)
-    aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.decode(x.to(dev)).cpu()
+    logits = torch.empty(64, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
     rows = torch.arange(0, 64, 8)
     want = ref.decode_routed(x[rows], aff[rows])
     check_close(got[rows], want, ties[rows], "decode 120b T=64 sample")

@@ -15,13 +15,18 @@
 
 #include "capi_util.h"
 #include "common.h"
+#include "router_dev.h"
 
 namespace mxmoe {
 
 constexpr int kTkgMaxT = 1024;
 constexpr int kTkgMaxE = 512;
 
-__global__ void __launch_bounds__(1024) tkg_route_kernel(
+// Routing of a decode batch by one workgroup of 1024 threads (thread t = token t):
+// per-expert slot lists with tokens ascending inside an expert (ranks from wave-wide
+// 64-bit masks and popcounts), the ascending list of active experts, and per token its
+// slots and weights sorted by expert id.
+__device__ __forceinline__ void tkg_route_block(
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_val, int T, int K, int E,
     int scale_mode, int32_t* __restrict__ expert_off, int32_t* __restrict__ active,
     int32_t* __restrict__ n_active, int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot,
@@ -91,9 +96,15 @@ __global__ void __launch_bounds__(1024) tkg_route_kernel(
   __syncthreads();
   if (tid >= T) return;
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int es[8], ss[8];
-  float ws[8];
+  // The token's selections in ascending expert id: selection k goes to position
+  // #{valid j : ids[j] < ids[k]} (ids are distinct); unused positions get -1.
   int n = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) n += (k < K && ids[k] >= 0) ? 1 : 0;
+  for (int k = n; k < K; ++k) {
+    tok_slot[(size_t)tid * K + k] = -1;
+    tok_w[(size_t)tid * K + k] = 0.f;
+  }
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (k >= K) break;
@@ -103,23 +114,90 @@ __global__ void __launch_bounds__(1024) tkg_route_kernel(
     for (int w = 0; w < wave; ++w) r += __popcll(masks[w][e]);
     r += __popcll(masks[wave][e] & below);
     slot_tok[r] = tid;
-    // insertion into the expert-ascending list
-    int p = n;
-    while (p > 0 && es[p - 1] > e) {
-      es[p] = es[p - 1];
-      ss[p] = ss[p - 1];
-      ws[p] = ws[p - 1];
-      --p;
+    int pos = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pos += (j < K && ids[j] >= 0 && ids[j] < e) ? 1 : 0;
+    tok_slot[(size_t)tid * K + pos] = r;
+    tok_w[(size_t)tid * K + pos] =
+        (scale_mode == MXMOE_SCALE_NO) ? (vals[k] > 0.f ? 1.f : 0.f) : vals[k];
+  }
+}
+
+__global__ void __launch_bounds__(1024) tkg_route_kernel(
+    const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_val, int T, int K, int E,
+    int scale_mode, int32_t* __restrict__ expert_off, int32_t* __restrict__ active,
+    int32_t* __restrict__ n_active, int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot,
+    float* __restrict__ tok_w) {
+  tkg_route_block(topk_idx, topk_val, T, K, E, scale_mode, expert_off, active, n_active, slot_tok,
+                  tok_slot, tok_w);
+}
+
+// Decode front end for small batches: router logits with one 16-wave workgroup per
+// 16 x 16 tile, then the top-k of each token (the routing kernel follows).
+constexpr int kFrontMaxT = 128;  // larger batches take the standalone router kernels
+
+// One workgroup (16 waves) per 16-token x 16-expert logits tile: the waves take the
+// 128-wide K chunks round-robin and their partial sums are added in wave order.
+// A = router rows (experts), B = tokens.
+__global__ void __launch_bounds__(1024) front_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias,
+                                                            float* __restrict__ logits, int T,
+                                                            int H, int E) {
+  __shared__ f32x4 red[16][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int q = lane >> 4, r16 = lane & 15;
+  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  const int nc = (H + 127) / 128, tail_q = (H % 128) / 32;
+  const uint16_t* xr = x + (size_t)min(t0 + r16, T - 1) * H;
+  const uint16_t* wr = w + (size_t)min(e0 + r16, E - 1) * H;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  for (int c = wave; c < nc; c += 16) {
+    const bool ok = (c < H / 128) || (q < tail_q);
+    const int k0 = ok ? c * 128 + q * 32 : 0;
+    u32x4 xv[4], wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[j] = *reinterpret_cast<const u32x4*>(xr + k0 + 8 * j);
+      wv[j] = *reinterpret_cast<const u32x4*>(wr + k0 + 8 * j);
     }
-    es[p] = e;
-    ss[p] = r;
-    ws[p] = (scale_mode == MXMOE_SCALE_NO) ? (vals[k] > 0.f ? 1.f : 0.f) : vals[k];
-    ++n;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[j] = ok ? xv[j] : zero4;
+      acc = mfma16(as_bf16x8(wv[j]), as_bf16x8(xv[j]), acc);
+    }
   }
-  for (int k = 0; k < K; ++k) {
-    tok_slot[(size_t)tid * K + k] = k < n ? ss[k] : -1;
-    tok_w[(size_t)tid * K + k] = k < n ? ws[k] : 0.f;
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (tid < 256) {
+    const int l = tid & 63, i = tid >> 6;  // D lane l, element i: expert 4(l/16)+i, token l%16
+    float v = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < 16; ++wv) v += red[wv][l][i];
+    const int tok = t0 + (l & 15), ex = e0 + 4 * (l >> 4) + i;
+    if (tok < T && ex < E) {
+      if (bias) v += bf16_bits_to_f32(bias[ex]);
+      logits[(size_t)tok * E + ex] = v;
+    }
   }
+}
+
+// Top-k of every token, one wave per token, four tokens per workgroup.
+template <int PER>
+__global__ void __launch_bounds__(256) front_topk_kernel(const float* __restrict__ logits, int T,
+                                                         int E, int K, int act, int act_first,
+                                                         int renorm, float renorm_eps,
+                                                         int32_t* __restrict__ topk_idx,
+                                                         float* __restrict__ topk_val) {
+  const int t = blockIdx.x * 4 + wave_id();
+  if (t >= T) return;
+  float v[PER];
+  load_row_wave<PER>(logits + (size_t)t * E, E, v);
+  int sel_idx[8];
+  float out[8];
+  topk_row_wave<PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+  store_topk_wave(sel_idx, out, K, topk_idx + (size_t)t * K, topk_val + (size_t)t * K);
 }
 
 __device__ __forceinline__ float clampf_ref(float v, float lo, float hi) {
@@ -571,11 +649,35 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
   decode_carve(workspace, workspace_bytes, T, H, I, E, top_k, &d);
   TkgWs w;
   tkg_carve(d.tkg, d.tkg_bytes, T, H, I, E, top_k, &w);
+  MXMOE_REQUIRE(router_act == MXMOE_ROUTER_SOFTMAX || router_act == MXMOE_ROUTER_SIGMOID,
+                "moe_decode: unknown router activation %d", router_act);
+  MXMOE_REQUIRE(H % 32 == 0, "moe_decode: H=%lld must be a multiple of 32", (long long)H);
   hipStream_t s = as_stream(stream);
+  float* logits = logits_out ? logits_out : d.logits;
   mark_event(stage_events, 0, s);
-  rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
-                  renorm_eps, logits_out ? logits_out : d.logits, nullptr, d.idx, d.val, s);
-  if (rc) return rc;
+  if (T <= kFrontMaxT) {
+    hipLaunchKernelGGL(front_logits_kernel,
+                       dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16)), dim3(1024), 0,
+                       s, x, router_w, router_b, logits, (int)T, (int)H, (int)E);
+    const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
+    const dim3 gt((unsigned)((T + 3) / 4));
+#define MXMOE_FRONT(P)                                                                      \
+  hipLaunchKernelGGL(front_topk_kernel<P>, gt, dim3(256), 0, s, logits, (int)T, (int)E, top_k, \
+                     router_act, af, rn, renorm_eps, d.idx, d.val)
+    switch (topk_per_lane((int)E)) {
+      case 1: MXMOE_FRONT(1); break;
+      case 2: MXMOE_FRONT(2); break;
+      case 4: MXMOE_FRONT(4); break;
+      default: MXMOE_FRONT(8); break;  // E <= 512 here
+    }
+#undef MXMOE_FRONT
+    rc = check_launch("moe_decode front end");
+    if (rc) return rc;
+  } else {
+    rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
+                    renorm_eps, logits, nullptr, d.idx, d.val, s);
+    if (rc) return rc;
+  }
   return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
                       top_k, act, clamps, scale_mode, out, w,
                       stage_events ? stage_events + 1 : nullptr, s);

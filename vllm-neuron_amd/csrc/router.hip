@@ -4,6 +4,7 @@
 
 #include "capi_util.h"
 #include "common.h"
+#include "router_dev.h"
 
 namespace mxmoe {
 
@@ -82,34 +83,8 @@ __global__ void __launch_bounds__(256) router_logits_kernel(
   }
 }
 
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-  // Larger value wins; equal values pick the lower index.  NaN never wins.
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    float ov = __shfl_xor(v, off);
-    int oi = __shfl_xor(idx, off);
-    if (ov > v || (ov == v && oi < idx)) {
-      v = ov;
-      idx = oi;
-    }
-  }
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
-
-constexpr int kMaxEPerLane = 16;  // E <= 1024
-
 // One wave per token: top-k over the row (desc., ties -> lower id), activation, scatter.
+template <int PER>
 __global__ void __launch_bounds__(256) router_topk_kernel(
     const float* __restrict__ logits, float* __restrict__ aff, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_val, int T, int E, int K, int act, int act_first, int renorm,
@@ -117,102 +92,11 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
   const int lane = threadIdx.x & 63;
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= T) return;
-  const float* row = logits + (size_t)tok * E;
-  float v[kMaxEPerLane];
-  const int per = (E + 63) / 64;
-#pragma unroll
-  for (int i = 0; i < kMaxEPerLane; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = (i < per && e < E) ? row[e] : -INFINITY;
-  }
-  float score[kMaxEPerLane];
-  if (act_first) {
-    if (act == MXMOE_ROUTER_SOFTMAX) {
-      float m = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < kMaxEPerLane; ++i)
-        if (i < per) m = fmaxf(m, v[i]);
-      m = wave_max(m);
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < kMaxEPerLane; ++i) {
-        const int e = lane + 64 * i;
-        score[i] = (i < per && e < E) ? expf(v[i] - m) : 0.f;
-        s += score[i];
-      }
-      s = wave_sum(s);
-#pragma unroll
-      for (int i = 0; i < kMaxEPerLane; ++i) {
-        const int e = lane + 64 * i;
-        score[i] = (i < per && e < E) ? score[i] / s : -INFINITY;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kMaxEPerLane; ++i) {
-        const int e = lane + 64 * i;
-        score[i] = (i < per && e < E) ? sigmoid_f32(v[i]) : -INFINITY;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < kMaxEPerLane; ++i) score[i] = v[i];
-  }
-  // k rounds of arg-max; selected entries are knocked out.
   int sel_idx[8];
-  float sel_val[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (k >= K) break;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < kMaxEPerLane; ++i) {
-      const int e = lane + 64 * i;
-      if (i < per && e < E && (score[i] > bv || (score[i] == bv && e < bi))) {
-        bv = score[i];
-        bi = e;
-      }
-    }
-    wave_argmax(bv, bi);
-    sel_idx[k] = bi;
-    sel_val[k] = bv;
-#pragma unroll
-    for (int i = 0; i < kMaxEPerLane; ++i)
-      if (lane + 64 * i == bi) score[i] = -INFINITY;
-  }
-  // Activation over the selected values unless it came first, then optional renorm.
   float out[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) out[k] = sel_val[k];
-  if (!act_first) {
-    if (act == MXMOE_ROUTER_SOFTMAX) {
-      const float m = sel_val[0];
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (k < K) {
-          out[k] = expf(sel_val[k] - m);
-          s += out[k];
-        }
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (k < K) out[k] = out[k] / s;
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (k < K) out[k] = sigmoid_f32(sel_val[k]);
-    }
-  }
-  if (renorm) {
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k < K) s += out[k];
-    s = s + renorm_eps;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k < K) out[k] = out[k] / s;
-  }
+  float vals[PER];
+  load_row_wave<PER>(logits + (size_t)tok * E, E, vals);
+  topk_row_wave<PER>(vals, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
   if (aff) {
     float* arow = aff + (size_t)tok * E;
     for (int e = lane; e < E; e += 64) {
@@ -223,18 +107,7 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
       arow[e] = a;
     }
   }
-  if (lane < K) {
-    int si = 0;
-    float so = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k == lane) {
-        si = sel_idx[k];
-        so = out[k];
-      }
-    topk_idx[(size_t)tok * K + lane] = si;
-    topk_val[(size_t)tok * K + lane] = so;
-  }
+  store_topk_wave(sel_idx, out, K, topk_idx + (size_t)tok * K, topk_val + (size_t)tok * K);
 }
 
 // One workgroup per token: x_norm = bf16(gamma * (x * rsqrt(mean(x[:ha]^2) + eps))).
@@ -295,9 +168,19 @@ int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64
   }
   int rc = check_launch("router_logits");
   if (rc) return rc;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, logits,
-                     affinities, topk_idx, topk_val, (int)T, (int)E, top_k, act,
-                     act_before_topk ? 1 : 0, renorm ? 1 : 0, renorm_eps);
+  const dim3 g((unsigned)((T + 3) / 4));
+  const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
+#define MXMOE_TOPK(P)                                                                          \
+  hipLaunchKernelGGL(router_topk_kernel<P>, g, dim3(256), 0, s, logits, affinities, topk_idx, \
+                     topk_val, (int)T, (int)E, top_k, act, af, rn, renorm_eps)
+  switch (topk_per_lane((int)E)) {
+    case 1: MXMOE_TOPK(1); break;
+    case 2: MXMOE_TOPK(2); break;
+    case 4: MXMOE_TOPK(4); break;
+    case 8: MXMOE_TOPK(8); break;
+    default: MXMOE_TOPK(16); break;
+  }
+#undef MXMOE_TOPK
   return check_launch("router_topk");
 }
 

@@ -1,0 +1,191 @@
+// Device helpers of the router shared by the standalone router kernels and the fused
+// decode front end: wave-wide reductions and the top-k of one logits row.
+#pragma once
+
+#include <math.h>
+
+#include "common.h"
+
+namespace mxmoe {
+
+constexpr int kMaxEPerLane = 16;  // E <= 1024
+
+// Wave-wide reductions through DPP lane moves (VALU latency, no LDS crossbar): within
+// each row of 16 lanes quad swaps, half-row and row mirrors; then row_bcast15/31 fold
+// rows 0..3 into lane 63, whose value is read into a scalar register (every lane gets
+// the same result).  Lanes a move has no source for keep the identity.
+#define MXMOE_DPP_STEP(T, OP, V, IDENT, CTRL, ROWS)                                            \
+  V = OP(V, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, IDENT), \
+                                                              __builtin_bit_cast(int, V),     \
+                                                              CTRL, ROWS, 0xf, false)))
+#define MXMOE_WAVE_REDUCE(T, OP, V, IDENT)                                                   \
+  do {                                                                                   \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0xB1, 0xf);  /* quad_perm [1,0,3,2] */              \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x4E, 0xf);  /* quad_perm [2,3,0,1] */              \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x141, 0xf); /* row_half_mirror */                   \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x140, 0xf); /* row_mirror */                        \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x142, 0xa); /* row_bcast15 into rows 1, 3 */        \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x143, 0xc); /* row_bcast31 into rows 2, 3 */        \
+  } while (0)
+
+__device__ __forceinline__ float fmax_op(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float fadd_op(float a, float b) { return a + b; }
+__device__ __forceinline__ int imin_op(int a, int b) { return a < b ? a : b; }
+
+__device__ __forceinline__ float wave_max(float v) {
+  MXMOE_WAVE_REDUCE(float, fmax_op, v, -INFINITY);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  MXMOE_WAVE_REDUCE(float, fadd_op, v, 0.0f);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ int wave_min(int v) {
+  MXMOE_WAVE_REDUCE(int, imin_op, v, 0x7fffffff);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Larger value wins; equal values pick the lower index.  A NaN value never wins (fmaxf
+// drops it and NaN == m is false); every lane gets the winner.  When one lane holds the
+// maximum its index is read directly; ties across lanes take a min-reduction.
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+  const float m = wave_max(v);
+  const unsigned long long at = __ballot(v == m);
+  if (__popcll(at) == 1)
+    idx = __builtin_amdgcn_readlane(idx, __ffsll((long long)at) - 1);
+  else
+    idx = wave_min(v == m ? idx : 0x7fffffff);
+  v = m;
+}
+
+// A row of E <= 64*PER logits into one wave: lane l holds experts l, l+64, ...
+template <int PER>
+__device__ __forceinline__ void load_row_wave(const float* __restrict__ row, int E,
+                                              float (&v)[PER]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : -INFINITY;
+  }
+}
+
+// Top-k of one row (as load_row_wave holds it) by one wave, router.py:383-565
+// semantics: act_first = 0: top-k on the logits (descending, equal values -> lower
+// expert id), then the activation over the k selected values; act_first = 1: the
+// activation over all E logits, then top-k.  renorm divides the k values by (their
+// sum + eps).  Every lane returns the same sel_idx[0..K) and out[0..K).
+template <int PER>
+__device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, int K, int act,
+                                              int act_first, int renorm, float renorm_eps,
+                                              int (&sel_idx)[8], float (&out)[8]) {
+  const int lane = threadIdx.x & 63;
+  float score[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) score[i] = vals[i];
+  if (act_first) {
+    if (act == MXMOE_ROUTER_SOFTMAX) {
+      float m = score[0];
+#pragma unroll
+      for (int i = 1; i < PER; ++i) m = fmaxf(m, score[i]);
+      m = wave_max(m);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        score[i] = lane + 64 * i < E ? expf(score[i] - m) : 0.f;
+        s += score[i];
+      }
+      s = wave_sum(s);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) score[i] = lane + 64 * i < E ? score[i] / s : -INFINITY;
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        score[i] = lane + 64 * i < E ? sigmoid_f32(score[i]) : -INFINITY;
+    }
+  }
+  // k rounds of arg-max; selected entries are knocked out.
+  float sel_val[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sel_idx[k] = 0;
+    sel_val[k] = 0.f;
+    if (k >= K) continue;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && (score[i] > bv || (score[i] == bv && e < bi))) {
+        bv = score[i];
+        bi = e;
+      }
+    }
+    wave_argmax(bv, bi);
+    sel_idx[k] = bi;
+    sel_val[k] = bv;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) score[i] = (lane + 64 * i == bi) ? -INFINITY : score[i];
+  }
+  // Activation over the selected values unless it came first, then optional renorm.
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = sel_val[k];
+  if (!act_first) {
+    if (act == MXMOE_ROUTER_SOFTMAX) {
+      const float m = sel_val[0];
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k < K) {
+          out[k] = expf(sel_val[k] - m);
+          s += out[k];
+        }
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k < K) out[k] = out[k] / s;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k < K) out[k] = sigmoid_f32(sel_val[k]);
+    }
+  }
+  if (renorm) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < K) s += out[k];
+    s = s + renorm_eps;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < K) out[k] = out[k] / s;
+  }
+}
+
+// Values per lane for E experts: the template argument of topk_row_wave.
+inline int topk_per_lane(int E) {
+  const int per = (E + 63) / 64;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+}
+
+// Lane k < K of the wave writes the k-th selection of a row.
+__device__ __forceinline__ void store_topk_wave(const int (&sel_idx)[8], const float (&out)[8],
+                                                int K, int32_t* __restrict__ idx_row,
+                                                float* __restrict__ val_row) {
+  const int lane = threadIdx.x & 63;
+  if (lane < K) {
+    int si = 0;
+    float so = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k == lane) {
+        si = sel_idx[k];
+        so = out[k];
+      }
+    idx_row[lane] = si;
+    val_row[lane] = so;
+  }
+}
+
+}  // namespace mxmoe
