@@ -21,6 +21,8 @@
 // combine: out[t] = bf16(sum over experts in ascending id of y * affinity) in fp32.
 #include <math.h>
 
+#include <type_traits>
+
 #include "capi_util.h"
 #include "common.h"
 
@@ -104,64 +106,85 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   const uint8_t* ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rg0 / 4) * q_sbytes;
   const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
 
-  // ---- global -> register staging assignment
-  // A: 4 pieces of 16 B per thread: row = 32*i + tid/16, col16 = tid%16
+  // ---- global -> register staging: every thread loads 4 x 16 B of activations
+  // (row 32*i + tid/16, 8 columns at 8*(tid%16)), 2 x 16 B of weights (row group
+  // tid/64 + 8*i, lane tid%64) and one word of scales (quad (tid/64)%4, lane tid%64;
+  // waves 4..7 repeat waves 0..3).  Loads are unconditional, from clamped addresses
+  // (padding slots read a real row, lanes past K read column 0, row groups past the
+  // tile read the first).  Two chunks are in flight.
   const int a_col = tid & 15, a_row0 = tid >> 4;
   const uint16_t* a_src[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 32 * i + a_row0;
     const int tk = stok[row];
-    if (tk < 0) a_src[i] = nullptr;
-    else if (GATE_UP) a_src[i] = args.a + (size_t)tk * K;
+    if (GATE_UP) a_src[i] = args.a + (size_t)(tk >= 0 ? tk : 0) * K;
     else a_src[i] = args.a + (size_t)(m0 + row) * K;
   }
-  // B: 2 pieces of 16 B: rg = (tid + 512 i) / 64, l16 = tid % 64
   const int b_l = tid & 63;
   const int b_rg0 = tid >> 6;  // + 8 i
-  // S: threads < 256, one word (a quad's 4 scale bytes) of lane s_l of quad s_q
-  const int s_q = tid >> 6, s_l = tid & 63;
+  const int s_q = (tid >> 6) & 3, s_l = tid & 63;
 
-  u32x4 ra[4], rbw[2];
-  uint32_t rs = 0;
+  struct Stage {
+    u32x4 a[4], b[2];
+    uint32_t s;
+  };
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
-  auto load_chunk = [&](int c) {
-    const int k0 = c * 128;
+  auto lane_in_k = [&](int c, int l) { return c < nfull || (l >> 4) < tail_q; };
+  auto load_chunk = [&](Stage& R, int c) {
+    const int kk = c * 128 + a_col * 8;
+    const int kc = kk < K ? kk : 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = k0 + a_col * 8;
-      ra[i] = (a_src[i] && kk < K) ? *reinterpret_cast<const u32x4*>(a_src[i] + kk) : zero4;
-    }
+    for (int i = 0; i < 4; ++i) R.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + kc);
+    const int bl = lane_in_k(c, b_l) ? b_l : 0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int rg = b_rg0 + 8 * i;
-      const bool ok = rg < rg_valid && (c < nfull || (b_l >> 4) < tail_q);
-      rbw[i] = ok ? *reinterpret_cast<const u32x4*>(wq + rg * rg_bytes + (size_t)c * 1024 + b_l * 16)
-                  : zero4;
+      const int rgc = rg < rg_valid ? rg : 0;
+      R.b[i] = *reinterpret_cast<const u32x4*>(wq + rgc * rg_bytes + (size_t)c * 1024 + bl * 16);
     }
-    if (tid < 256) {
-      const bool ok = 4 * s_q < rg_valid && (c < nfull || (s_l >> 4) < tail_q);
-      rs = ok ? *reinterpret_cast<const uint32_t*>(ws + s_q * q_sbytes + (size_t)c * 256 + s_l * 4)
-              : 0u;
-    }
+    const int sq = 4 * s_q < rg_valid ? s_q : 0;
+    const int sl = lane_in_k(c, s_l) ? s_l : 0;
+    R.s = *reinterpret_cast<const uint32_t*>(ws + sq * q_sbytes + (size_t)c * 256 + sl * 4);
   };
-  auto store_chunk = [&](int st) {
+  // Activations are stored as loaded: an MFMA output column depends on its own slot
+  // only, so padding slots (and their unwritten h rows) touch discarded columns, and
+  // the column-0 values that lanes past K hold meet zero weights.  Row groups past
+  // the tile give discarded rows.  Only the partial last K chunk needs zeroing: its
+  // weights (and scales, so no scale byte of 255 turns a zero into NaN).
+  auto store_chunk = [&](const Stage& R, int c, int st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&sa[st][(32 * i + a_row0) * kARow + a_col * 16]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<u32x4*>(&sb[st][(b_rg0 + 8 * i) * 1024 + b_l * 16]) = rbw[i];
-    if (tid < 256) *reinterpret_cast<uint32_t*>(&ss[st][s_q * 256 + s_l * 4]) = rs;
+      *reinterpret_cast<u32x4*>(&sa[st][(32 * i + a_row0) * kARow + a_col * 16]) = R.a[i];
+    u32x4 b0 = R.b[0], b1 = R.b[1];
+    uint32_t sw = R.s;
+    if (c >= nfull) {  // wave-uniform
+      const bool bok = lane_in_k(c, b_l);
+      b0 = bok ? b0 : zero4;
+      b1 = bok ? b1 : zero4;
+      sw = lane_in_k(c, s_l) ? sw : 0u;
+    }
+    *reinterpret_cast<u32x4*>(&sb[st][b_rg0 * 1024 + b_l * 16]) = b0;
+    *reinterpret_cast<u32x4*>(&sb[st][(b_rg0 + 8) * 1024 + b_l * 16]) = b1;
+    // waves 4..7 write the same words as waves 0..3 (same values)
+    *reinterpret_cast<uint32_t*>(&ss[st][s_q * 256 + s_l * 4]) = sw;
   };
 
   const int wm = wave & 1, wn = wave >> 1;
-  // Wave-uniform activity: its row groups exist and one of its 64 slots is real.
-  bool wave_rows = (4 * wn) < rg_valid;
-  bool wave_slots = false;
-  for (int i = 0; i < 64; ++i) wave_slots |= stok[64 * wm + i] >= 0;
-  const bool active = wave_rows && wave_slots;
+  // Wave-uniform activity: its row groups exist; ntv = its 16-slot MFMA tiles that
+  // hold a real slot (real slots of a block come first, so they are a prefix).
+  const bool wave_rows = (4 * wn) < rg_valid;
+  int nvalid = 0;
+  for (int i = 0; i < 64; ++i) nvalid += stok[64 * wm + i] >= 0 ? 1 : 0;
+  int ntv = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    bool any = false;
+    for (int i = 0; i < 16; ++i) any |= stok[64 * wm + 16 * t + i] >= 0;
+    ntv = any ? t + 1 : ntv;
+  }
+  const bool active = wave_rows && nvalid > 0;
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -169,38 +192,56 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  load_chunk(0);
-  store_chunk(0);
-  __syncthreads();
-  for (int c = 0; c < nc; ++c) {
-    const int st = c & 1;
-    if (c + 1 < nc) load_chunk(c + 1);
-    if (active) {
-      u32x4 wv[4];
-      float sc[4];
-      const uint32_t s4 = *reinterpret_cast<const uint32_t*>(&ss[st][wn * 256 + lane * 4]);
+  // NTV MFMA tiles of 16 slots per 64-slot wave tile; the rest are padding.
+  auto compute = [&](auto ntv_c, int st) {
+    constexpr int NTV = decltype(ntv_c)::value;
+    u32x4 wv[4];
+    float sc[4];
+    const uint32_t s4 = *reinterpret_cast<const uint32_t*>(&ss[st][wn * 256 + lane * 4]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wv[r] = *reinterpret_cast<const u32x4*>(&sb[st][(4 * wn + r) * 1024 + lane * 16]);
+      sc[r] = e8m0_to_f32((s4 >> (8 * r)) & 0xffu);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 xv[NTV];
+#pragma unroll
+      for (int t = 0; t < NTV; ++t)
+        xv[t] = *reinterpret_cast<const u32x4*>(
+            &sa[st][(64 * wm + 16 * t + (lane & 15)) * kARow + (32 * q + 8 * j) * 2]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        wv[r] = *reinterpret_cast<const u32x4*>(&sb[st][(4 * wn + r) * 1024 + lane * 16]);
-        sc[r] = e8m0_to_f32((s4 >> (8 * r)) & 0xffu);
-      }
+        const bf16x8 wf = dequant8(wv[r][j], sc[r]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x4 xv[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          xv[t] = *reinterpret_cast<const u32x4*>(
-              &sa[st][(64 * wm + 16 * t + (lane & 15)) * kARow + (32 * q + 8 * j) * 2]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bf16x8 wf = dequant8(wv[r][j], sc[r]);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) acc[r][t] = mfma16(wf, as_bf16x8(xv[t]), acc[r][t]);
-        }
+        for (int t = 0; t < NTV; ++t) acc[r][t] = mfma16(wf, as_bf16x8(xv[t]), acc[r][t]);
       }
     }
-    if (c + 1 < nc) store_chunk(st ^ 1);
+  };
+  // The whole K loop per tile count, so no branch sits between the MFMAs.
+  auto main_loop = [&](auto ntv_c) {
+    Stage R0, R1;
+    load_chunk(R0, 0);
+    load_chunk(R1, nc > 1 ? 1 : 0);
+    store_chunk(R0, 0, 0);
     __syncthreads();
+    for (int c = 0; c < nc; c += 2) {
+      load_chunk(R0, c + 2 < nc ? c + 2 : nc - 1);
+      if (active) compute(ntv_c, 0);
+      if (c + 1 < nc) store_chunk(R1, c + 1, 1);
+      __syncthreads();
+      if (c + 1 >= nc) break;
+      load_chunk(R1, c + 3 < nc ? c + 3 : nc - 1);
+      if (active) compute(ntv_c, 1);
+      if (c + 2 < nc) store_chunk(R0, c + 2, 0);
+      __syncthreads();
+    }
+  };
+  switch (ntv) {
+    case 1: main_loop(std::integral_constant<int, 1>()); break;
+    case 2: main_loop(std::integral_constant<int, 2>()); break;
+    case 3: main_loop(std::integral_constant<int, 3>()); break;
+    default: main_loop(std::integral_constant<int, 4>()); break;
   }
   if (!active) return;
 
