@@ -29,8 +29,7 @@
 namespace mxmoe {
 
 constexpr int kPM = 128;    // slots per M-tile
-constexpr int kPRG = 16;    // row groups per N-tile (256 rows)
-constexpr int kARow = 272;  // LDS bytes per activation row of a chunk (256 + 16 pad)
+constexpr int kPRG = 32;    // row groups per N-tile (512 rows), 8 per wave
 constexpr int kPThreads = 512;
 
 struct PrefillArgs {
@@ -67,9 +66,15 @@ __device__ __forceinline__ float act_bf16(float g, int act) {
 
 template <bool GATE_UP>
 __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs args) {
-  __shared__ __attribute__((aligned(16))) uint8_t sa[2][kPM * kARow];
-  __shared__ __attribute__((aligned(16))) uint8_t sb[2][kPRG * 1024];
-  __shared__ __attribute__((aligned(16))) uint8_t ss[2][kPRG * 64];
+  constexpr int WR = kPRG / 4;  // row groups per wave (4 waves across N)
+  constexpr int NQ = kPRG / 4;  // scale quads per tile
+  static_assert(NQ == kPThreads / 64, "one scale quad per wave");
+  // The two pipeline stages are separate arrays indexed at compile time: the
+  // compiler then tells the stage being read from the one a direct load is filling
+  // and waits only for the former.
+  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256];
+  __shared__ __attribute__((aligned(1024))) uint8_t sb0[kPRG * 1024], sb1[kPRG * 1024];
+  __shared__ __attribute__((aligned(1024))) uint8_t ss0[NQ * 256], ss1[NQ * 256];
   __shared__ int32_t stok[kPM];
   __shared__ int s_any;
 
@@ -100,83 +105,60 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   const int K = args.K;
   const size_t rg_bytes = (size_t)K * 8, q_sbytes = (size_t)K * 2;
   const int n_rg_total = args.N_rows / 16;
-  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds 4 scale quads
+  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds NQ scale quads
   const int rg_valid = min(kPRG, n_rg_total - rg0);
   const uint8_t* wq = args.wq + ((size_t)e * n_rg_total + rg0) * rg_bytes;
   const uint8_t* ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rg0 / 4) * q_sbytes;
   const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
+  auto lane_in_k = [&](int c, int l) { return c < nfull || (l >> 4) < tail_q; };
 
-  // ---- global -> register staging: every thread loads 4 x 16 B of activations
-  // (row 32*i + tid/16, 8 columns at 8*(tid%16)), 2 x 16 B of weights (row group
-  // tid/64 + 8*i, lane tid%64) and one word of scales (quad (tid/64)%4, lane tid%64;
-  // waves 4..7 repeat waves 0..3).  Loads are unconditional, from clamped addresses
-  // (padding slots read a real row, lanes past K read column 0, row groups past the
-  // tile read the first).  Two chunks are in flight.
-  const int a_col = tid & 15, a_row0 = tid >> 4;
-  const uint16_t* a_src[4];
+  // ---- global -> LDS, no registers: each wave issues 4 x 1 KiB of activations (rows
+  // 16w + 4i + lane/16), 4 x 1 KiB of weights (row groups 4w + i) and 256 B of
+  // scales (quad w) per chunk.  A chunk row of activations (128 bf16) is 16 blocks of
+  // 16 B; block cb of row r sits at slot cb ^ (r % 16), so the 16 rows an MFMA reads
+  // hit 16 different slots (no bank conflicts) without padding.  Addresses are
+  // clamped to real data (padding slots read token 0, columns past K read block 0,
+  // row groups past the tile read the first): an MFMA output column depends on its
+  // own slot only and discarded rows are never stored, and compute() gives lanes past
+  // K a zero scale so their weights add nothing.
+  const uint16_t* a_row[4];
+  int a_swz[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 32 * i + a_row0;
+    const int row = 16 * wave + 4 * i + (lane >> 4);
     const int tk = stok[row];
-    if (GATE_UP) a_src[i] = args.a + (size_t)(tk >= 0 ? tk : 0) * K;
-    else a_src[i] = args.a + (size_t)(m0 + row) * K;
+    a_row[i] = GATE_UP ? args.a + (size_t)(tk >= 0 ? tk : 0) * K
+                       : args.a + (size_t)(m0 + row) * K;
+    a_swz[i] = (lane & 15) ^ (row & 15);  // the column block this lane's slot holds
   }
-  const int b_l = tid & 63;
-  const int b_rg0 = tid >> 6;  // + 8 i
-  const int s_q = (tid >> 6) & 3, s_l = tid & 63;
-
-  struct Stage {
-    u32x4 a[4], b[2];
-    uint32_t s;
-  };
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
-
-  auto lane_in_k = [&](int c, int l) { return c < nfull || (l >> 4) < tail_q; };
-  auto load_chunk = [&](Stage& R, int c) {
-    const int kk = c * 128 + a_col * 8;
-    const int kc = kk < K ? kk : 0;
+  auto issue_chunk = [&](auto st_c, int c) {
+    constexpr int ST = decltype(st_c)::value;
+    uint8_t* sa = ST ? sa1 : sa0;
+    uint8_t* sb = ST ? sb1 : sb0;
+    uint8_t* ss = ST ? ss1 : ss0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) R.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + kc);
-    const int bl = lane_in_k(c, b_l) ? b_l : 0;
+    for (int i = 0; i < 4; ++i) {
+      const int kcol = c * 128 + a_swz[i] * 8;
+      const uint16_t* src = a_row[i] + (kcol < K ? kcol : a_swz[i] * 8);
+      __builtin_amdgcn_global_load_lds(src, &sa[(16 * wave + 4 * i) * 256], 16, 0, 0);
+    }
+    const int bl = lane_in_k(c, lane) ? lane : 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int rg = b_rg0 + 8 * i;
+    for (int i = 0; i < 4; ++i) {
+      const int rg = 4 * wave + i;
       const int rgc = rg < rg_valid ? rg : 0;
-      R.b[i] = *reinterpret_cast<const u32x4*>(wq + rgc * rg_bytes + (size_t)c * 1024 + bl * 16);
+      __builtin_amdgcn_global_load_lds(wq + rgc * rg_bytes + (size_t)c * 1024 + bl * 16,
+                                       &sb[rg * 1024], 16, 0, 0);
     }
-    const int sq = 4 * s_q < rg_valid ? s_q : 0;
-    const int sl = lane_in_k(c, s_l) ? s_l : 0;
-    R.s = *reinterpret_cast<const uint32_t*>(ws + sq * q_sbytes + (size_t)c * 256 + sl * 4);
-  };
-  // Activations are stored as loaded: an MFMA output column depends on its own slot
-  // only, so padding slots (and their unwritten h rows) touch discarded columns, and
-  // the column-0 values that lanes past K hold meet zero weights.  Row groups past
-  // the tile give discarded rows.  Only the partial last K chunk needs zeroing: its
-  // weights (and scales, so no scale byte of 255 turns a zero into NaN).
-  auto store_chunk = [&](const Stage& R, int c, int st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(&sa[st][(32 * i + a_row0) * kARow + a_col * 16]) = R.a[i];
-    u32x4 b0 = R.b[0], b1 = R.b[1];
-    uint32_t sw = R.s;
-    if (c >= nfull) {  // wave-uniform
-      const bool bok = lane_in_k(c, b_l);
-      b0 = bok ? b0 : zero4;
-      b1 = bok ? b1 : zero4;
-      sw = lane_in_k(c, s_l) ? sw : 0u;
-    }
-    *reinterpret_cast<u32x4*>(&sb[st][b_rg0 * 1024 + b_l * 16]) = b0;
-    *reinterpret_cast<u32x4*>(&sb[st][(b_rg0 + 8) * 1024 + b_l * 16]) = b1;
-    // waves 4..7 write the same words as waves 0..3 (same values)
-    *reinterpret_cast<uint32_t*>(&ss[st][s_q * 256 + s_l * 4]) = sw;
+    const int qc = 4 * wave < rg_valid ? wave : 0;
+    __builtin_amdgcn_global_load_lds(ws + qc * q_sbytes + (size_t)c * 256 + bl * 4,
+                                     &ss[wave * 256], 4, 0, 0);
   };
 
   const int wm = wave & 1, wn = wave >> 1;
   // Wave-uniform activity: its row groups exist; ntv = its 16-slot MFMA tiles that
   // hold a real slot (real slots of a block come first, so they are a prefix).
-  const bool wave_rows = (4 * wn) < rg_valid;
-  int nvalid = 0;
-  for (int i = 0; i < 64; ++i) nvalid += stok[64 * wm + i] >= 0 ? 1 : 0;
+  const bool wave_rows = (WR * wn) < rg_valid;
   int ntv = 0;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -184,57 +166,68 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     for (int i = 0; i < 16; ++i) any |= stok[64 * wm + 16 * t + i] >= 0;
     ntv = any ? t + 1 : ntv;
   }
-  const bool active = wave_rows && nvalid > 0;
+  const bool active = wave_rows && ntv > 0;
 
-  f32x4 acc[4][4];
+  f32x4 acc[WR][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < WR; ++r)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // NTV MFMA tiles of 16 slots per 64-slot wave tile; the rest are padding.
-  auto compute = [&](auto ntv_c, int st) {
+  // A wave computes 64 slots (NTV tiles of 16 hold real ones) x WR row groups.
+  auto compute = [&](auto ntv_c, auto st_c, int c) {
     constexpr int NTV = decltype(ntv_c)::value;
-    u32x4 wv[4];
-    float sc[4];
-    const uint32_t s4 = *reinterpret_cast<const uint32_t*>(&ss[st][wn * 256 + lane * 4]);
+    constexpr int ST = decltype(st_c)::value;
+    const uint8_t* sa = ST ? sa1 : sa0;
+    const uint8_t* sb = ST ? sb1 : sb0;
+    const uint8_t* ss = ST ? ss1 : ss0;
+    const bool kok = lane_in_k(c, lane);
+    float sc[WR];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      wv[r] = *reinterpret_cast<const u32x4*>(&sb[st][(4 * wn + r) * 1024 + lane * 16]);
-      sc[r] = e8m0_to_f32((s4 >> (8 * r)) & 0xffu);
+    for (int h = 0; h < WR / 4; ++h) {
+      const uint32_t s4 =
+          *reinterpret_cast<const uint32_t*>(&ss[(WR / 4 * wn + h) * 256 + lane * 4]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sc[4 * h + r] = kok ? e8m0_to_f32((s4 >> (8 * r)) & 0xffu) : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int slot = (4 * q + j) ^ (lane & 15);
       u32x4 xv[NTV];
 #pragma unroll
       for (int t = 0; t < NTV; ++t)
         xv[t] = *reinterpret_cast<const u32x4*>(
-            &sa[st][(64 * wm + 16 * t + (lane & 15)) * kARow + (32 * q + 8 * j) * 2]);
+            &sa[(64 * wm + 16 * t + (lane & 15)) * 256 + slot * 16]);
+      // dword j of each row group's 16 bytes: 8 weights of this MFMA step
+      uint32_t wj[WR];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bf16x8 wf = dequant8(wv[r][j], sc[r]);
+      for (int r = 0; r < WR; ++r)
+        wj[r] = *reinterpret_cast<const uint32_t*>(&sb[(WR * wn + r) * 1024 + lane * 16 + 4 * j]);
+#pragma unroll
+      for (int r = 0; r < WR; ++r) {
+        const bf16x8 wf = dequant8(wj[r], sc[r]);
 #pragma unroll
         for (int t = 0; t < NTV; ++t) acc[r][t] = mfma16(wf, as_bf16x8(xv[t]), acc[r][t]);
       }
     }
   };
-  // The whole K loop per tile count, so no branch sits between the MFMAs.
+  // The whole K loop per tile count, so no branch sits between the MFMAs.  Chunk
+  // c + 1 streams into the other LDS stage while chunk c computes; the barrier at
+  // the top of each half waits (its release fence) for the chunk about to be read
+  // and for every wave to be done with the stage about to be refilled.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   auto main_loop = [&](auto ntv_c) {
-    Stage R0, R1;
-    load_chunk(R0, 0);
-    load_chunk(R1, nc > 1 ? 1 : 0);
-    store_chunk(R0, 0, 0);
-    __syncthreads();
+    issue_chunk(S0(), 0);
     for (int c = 0; c < nc; c += 2) {
-      load_chunk(R0, c + 2 < nc ? c + 2 : nc - 1);
-      if (active) compute(ntv_c, 0);
-      if (c + 1 < nc) store_chunk(R1, c + 1, 1);
       __syncthreads();
+      if (c + 1 < nc) issue_chunk(S1(), c + 1);
+      if (active) compute(ntv_c, S0(), c);
       if (c + 1 >= nc) break;
-      load_chunk(R1, c + 3 < nc ? c + 3 : nc - 1);
-      if (active) compute(ntv_c, 1);
-      if (c + 2 < nc) store_chunk(R0, c + 2, 0);
       __syncthreads();
+      if (c + 2 < nc) issue_chunk(S0(), c + 2);
+      if (active) compute(ntv_c, S1(), c + 1);
     }
   };
   switch (ntv) {
@@ -249,9 +242,9 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   if (GATE_UP) {
     const int I = args.I;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
-      if (4 * wn + 2 * pp >= rg_valid) continue;
-      const int P = (rg0 + 4 * wn) / 2 + pp;  // pair index = 16 intermediate columns
+    for (int pp = 0; pp < WR / 2; ++pp) {
+      if (WR * wn + 2 * pp >= rg_valid) continue;
+      const int P = (rg0 + WR * wn) / 2 + pp;  // pair index = 16 intermediate columns
       const int col0 = 16 * P + 4 * q;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -277,9 +270,9 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   } else {
     const int H = args.H;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (4 * wn + r >= rg_valid) continue;
-      const int n0 = 16 * (rg0 + 4 * wn + r) + 4 * q;
+    for (int r = 0; r < WR; ++r) {
+      if (WR * wn + r >= rg_valid) continue;
+      const int n0 = 16 * (rg0 + WR * wn + r) + 4 * q;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int row = 64 * wm + 16 * t + (lane & 15);
