@@ -89,3 +89,20 @@ def test_moe_cte_api_padding_and_skip_token(dev):
                              activation_function="Swish")
     assert torch.all(got[150:] == 0)
     check_close(got[:150], want[:150], None, "moe_cte padding mask")
+
+
+def test_prefill_and_decode_partial_chunks(dev):
+    """K below one 128-wide chunk (gate_up, H = 96) and a partial last chunk (down,
+    I = 160); 6 row groups of H leave a partial scale quad."""
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape("smallk", 8, 2, 96, 160)
+    ref, layer, _ = build(shape, 51, dev, exp=(118, 122))
+    x = synthetic.tokens(52, 70, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev), output_dtype=torch.float32).cpu()
+    want, _ = ref.prefill(x, aff)
+    check_close(got, want, ties, "prefill small K")
+    got = layer.decode(x.to(dev)).cpu()
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, "decode small K")

@@ -1,16 +1,17 @@
 // Prefill (context encoding) expert MLP over the blockwise mapping.
 //
 // Both projections run the same LDS-tiled grouped GEMM:
-//   workgroup tile = 128 slots (M) x 256 weight rows (N, 16 row groups) x 128-wide
-//   K chunks, 8 waves as 2 (M) x 4 (N), each wave 64 slots x 64 rows = 4 x 4
-//   MFMA 16x16x32 tiles.  A chunk of activations (128 x 128 bf16, rows padded to
-//   272 bytes against bank conflicts) and of packed weights (16 x 1 KiB + 16 x 64
-//   scale bytes) is staged per step, double-buffered with one barrier per step;
-//   the next chunk's global loads are in flight while the current one computes.
+//   workgroup tile = 128 slots (M) x 512 weight rows (N, 32 row groups) x 128-wide
+//   K chunks; 8 waves as 2 (M) x 4 (N), each wave 64 slots x 128 rows = 8 x 4
+//   MFMA 16x16x32 tiles.  Per chunk the workgroup moves 32 KiB of activations (bf16,
+//   16-byte blocks XOR-swizzled by row against bank conflicts), 32 KiB of packed
+//   weights and 2 KiB of scales from global memory straight into LDS (no register
+//   staging), two stages deep: chunk c + 1 streams in while chunk c computes.
 //   Weights are dequantized from LDS to bf16 in registers by the CDNA4 scaled
 //   conversion, right before the MFMAs.
 //   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one
-//   expert; tiles whose 128 slots are all padding exit at once.  Tiles are
+//   expert; tiles whose 128 slots are all padding exit at once, and inside a tile
+//   each wave runs only the 16-slot MFMA tiles that hold real slots.  Tiles are
 //   ordered N-fastest and dealt out XCD by XCD, so the workgroups sharing an
 //   M-tile's activations (and an expert's weights) sit on the same L2.
 // gate_up: A = x rows gathered through token_position_to_id; epilogue = bias,
@@ -117,7 +118,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   // scales (quad w) per chunk.  A chunk row of activations (128 bf16) is 16 blocks of
   // 16 B; block cb of row r sits at slot cb ^ (r % 16), so the 16 rows an MFMA reads
   // hit 16 different slots (no bank conflicts) without padding.  Addresses are
-  // clamped to real data (padding slots read token 0, columns past K read block 0,
+  // clamped to real data (padding slots read token 0, columns past K read column 0,
   // row groups past the tile read the first): an MFMA output column depends on its
   // own slot only and discarded rows are never stored, and compute() gives lanes past
   // K a zero scale so their weights add nothing.
@@ -139,7 +140,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kcol = c * 128 + a_swz[i] * 8;
-      const uint16_t* src = a_row[i] + (kcol < K ? kcol : a_swz[i] * 8);
+      const uint16_t* src = a_row[i] + (kcol < K ? kcol : 0);  // column 0: in the row
       __builtin_amdgcn_global_load_lds(src, &sa[(16 * wave + 4 * i) * 256], 16, 0, 0);
     }
     const int bl = lane_in_k(c, lane) ? lane : 0;
