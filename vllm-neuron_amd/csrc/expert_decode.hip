@@ -213,23 +213,23 @@ __device__ __forceinline__ float act_f32(float g, int act) {
   return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
 }
 
-// Registers of one K chunk of a streamed tile: R = 4 weight row groups (16 B per
-// lane each), their four scale bytes (one 32-bit word per lane: the packed scales
-// keep a quad of row groups together) and NT token tiles of activations (4 x 16 B
-// per lane; with SPLIT a second (lo) copy).
+// Registers of one K chunk of a streamed tile: R weight row groups (16 B per lane
+// each), their scale bytes (one 32-bit word per lane and quad of row groups: the
+// packed scales keep quads together) and NT token tiles of activations (4 x 16 B per
+// lane; with SPLIT a second (lo) copy).
 template <int R, int NT, bool SPLIT>
 struct ChunkFrag {
-  static_assert(R == 4, "a streamed tile is one quad of row groups");
+  static_assert(R % 4 == 0, "a streamed tile is whole quads of row groups");
   u32x4 w[R];
-  uint32_t s;
+  uint32_t s[R / 4];
   u32x4 b[NT][4];
   u32x4 b2[SPLIT ? NT : 1][4];
 };
 
 struct StreamGeom {
   const uint8_t* wq;  // first row group of the tile
-  const uint8_t* ws;  // the tile's quad of scales
-  size_t rg_bytes;
+  const uint8_t* ws;  // the tile's first quad of scales
+  uint32_t rg_bytes, q_bytes;
   int rv;             // valid row groups in the tile (<= R)
   int nfull, tail_q;  // full 128-wide chunks, 32-blocks in the partial last chunk
 };
@@ -250,13 +250,19 @@ __device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, co
   const uint32_t lo = ok ? (uint32_t)lane : 0u;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int rr = r < g.rv ? r : g.rv - 1;
-    const uint8_t* wb = g.wq + rr * g.rg_bytes + (size_t)c * 1024;  // wave-uniform
-    // Weights are read once per step: non-temporal, so they do not evict the
-    // activations and scales that neighbouring waves re-read from the caches.
-    f.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wb + lo * 16u));
+    const uint32_t rr = r < g.rv ? r : g.rv - 1;
+    // One wave-uniform base and a 32-bit offset per lane.  Weights are read once per
+    // step: non-temporal, so they do not evict the activations and scales that
+    // neighbouring waves re-read from the caches.
+    const uint32_t off = rr * g.rg_bytes + (uint32_t)c * 1024u + lo * 16u;
+    f.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + off));
   }
-  f.s = *reinterpret_cast<const uint32_t*>(g.ws + (size_t)c * 256 + lo * 4u);
+#pragma unroll
+  for (int h = 0; h < R / 4; ++h) {
+    const uint32_t qq = 4 * h < g.rv ? h : 0;  // a partial last tile stays in its expert
+    f.s[h] = *reinterpret_cast<const uint32_t*>(g.ws + qq * g.q_bytes + (uint32_t)c * 256u +
+                                                lo * 4u);
+  }
   const uint32_t k0b = ok ? (uint32_t)(c * 128 + q * 32) * 2u : 0u;  // byte offset in a row
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -278,7 +284,7 @@ __device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int 
   const bool ok = (c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float sc = ok ? e8m0_to_f32((f.s >> (8 * r)) & 0xffu) : 0.0f;
+    const float sc = ok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 wf = dequant8(f.w[r][j], sc);
@@ -356,14 +362,15 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   const int n_rg = GATE_UP ? (2 * I) / 16 : H / 16;
   const int nc = (K + 127) / 128;
   StreamGeom g;
-  g.rg_bytes = (size_t)K * 8;
+  g.rg_bytes = (uint32_t)K * 8u;
+  g.q_bytes = (uint32_t)K * 2u;
   g.nfull = K / 128;
   g.tail_q = (K % 128) / 32;
   const int ai = item / ipe, ri = item - ai * ipe;
   // Item metadata is wave-uniform: keep it in scalar registers.
   const int e = __builtin_amdgcn_readfirstlane(a.active[ai]);
   const int rg0 = ri * R;
-  g.wq = a.wq + ((size_t)e * n_rg + rg0) * g.rg_bytes;
+  g.wq = a.wq + ((size_t)e * n_rg + rg0) * (size_t)g.rg_bytes;
   g.ws = a.ws + ((size_t)e * ((n_rg + 3) / 4) + rg0 / 4) * (size_t)(2 * K);
   g.rv = min(R, n_rg - rg0);
   const int s0 = __builtin_amdgcn_readfirstlane(a.expert_off[e]);
@@ -562,10 +569,18 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     return dim3((unsigned)((E * tkg_items_per_expert((int)H, (int)I, gate_up, R) + 3) / 4));
   };
   // Token tiles per pass: an expert with more tokens loops over passes.
+  // down with 8 row groups per item halves its activation loads per weight byte; it
+  // pays off while the item count still fills the GPU (expected active experts
+  // E (1 - (1 - k/E)^T) from the batch size).
+  const double active_est = (double)E * (1.0 - pow(1.0 - (double)top_k / (double)E, (double)T));
+  const bool down8 = active_est * (double)(H / 16) / 8.0 >= 2048.0;
   if (T <= 16 || T * top_k <= 8 * E) {
     hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
     mark_event(ev, 2, s);
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
+    if (down8)
+      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 2>), grid(false, 8), dim3(256), 0, s, dn);
+    else
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
   } else {
     hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
     mark_event(ev, 2, s);
