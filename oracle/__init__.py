@@ -15,6 +15,8 @@ reference's own CPU implementation of the MXFP4 MoE path (vllm-neuron, CPU mode)
     (vllm_neuron/functional/moe/moe_block_tkg.py:56-302)              -> oracle.moe_block_tkg
   * the GPT-OSS expert-layer orchestration of those calls
     (vllm_neuron/model/gpt_oss/model_bf16.py:1199-1413)               -> oracle.layer
+  * the load-time transform into the Trainium kernel layout (one rank)
+    (vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:243-885)       -> oracle.neuron_layout
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker (or, for the

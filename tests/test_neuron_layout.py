@@ -1,0 +1,121 @@
+"""Converter from the reference's Trainium MXFP4 kernel layout (CPU).
+
+oracle.neuron_layout restates the reference loaders' forward transform; it is pinned
+here by the reference's docstring examples and by an index formula worked out from
+the reshape/permute semantics.  The product converter must invert it exactly and
+give the same packed experts as packing the checkpoint directly."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import neuron_layout as onl
+
+
+def test_docstring_examples():
+    # _get_i_tiling_shard_i (weight_loaders_mxfp4.py:856-860): I=1536 at TP4, I=1024 at TP2
+    assert onl.i_tiling(1536 // 4) == (1, 12)
+    assert onl.i_tiling(1024 // 2) == (1, 16)
+    # get_shard_deinterleaved (utils/weight_loader.py:869-874) at one shard
+    t = torch.tensor([[10, 20, 11, 21, 12, 22, 13, 23]])  # g0 u0 g1 u1 ...
+    g, u = onl.deinterleave(t, 1)
+    assert g.tolist() == [[10, 11, 12, 13]] and u.tolist() == [[20, 21, 22, 23]]
+    # _pack_fp4_x4_uint16 (:575-576): the uint16 holds the same bytes in memory order
+    b = torch.tensor([0x01, 0x23, 0x45, 0x67], dtype=torch.uint8)
+    p = onl.pack_fp4_x4_uint16(b)
+    assert p.shape == (2,) and bytes(p.numpy().tobytes()) == bytes([0x01, 0x23, 0x45, 0x67])
+
+
+def test_gate_up_blocks_index_formula():
+    E, Hp, Ip = 1, 1024, 1024  # 2 H tiles, 2 I tiles
+    x = torch.arange(E * (Hp // 4) * 2 * Ip, dtype=torch.int64).reshape(E, Hp // 4, 2 * Ip)
+    out = onl.tile_gate_up_blocks(x).numpy()
+    nHt, qbH = onl.h_tiling(Hp)
+    nIt, qbI = onl.i_tiling(Ip)
+    idx = np.indices(out.shape)
+    e, p, g, ht, f = idx
+    qb, qh = p // 8, p % 8
+    it, rest = f // (4 * qbI * 8), f % (4 * qbI * 8)
+    qw, rest = rest // (qbI * 8), rest % (qbI * 8)
+    qbi, qhi = rest // 8, rest % 8
+    hq = (ht * qbH + qb) * 8 + qh
+    j = (((g * nIt + it) * qbI + qbi) * 8 + qhi) * 4 + qw
+    assert np.array_equal(out, x.numpy()[e, hq, j])
+
+
+def test_down_blocks_index_formula():
+    E, Hp, Ip = 1, 512, 1024
+    x = torch.arange(E * (Ip // 4) * Hp, dtype=torch.int64).reshape(E, Ip // 4, Hp)
+    out = onl.tile_down_blocks(x).numpy()
+    nIt, qbI = onl.i_tiling(Ip)
+    e, p, it, f = np.indices(out.shape)
+    qbi, qh = p // 8, p % 8
+    hb, hn = f // (Hp // 4), f % (Hp // 4)  # shuffled H: [4, H/4]
+    iq = (it * qbI + qbi) * 8 + qh
+    h = hn * 4 + hb
+    assert np.array_equal(out, x.numpy()[e, iq, h])
+
+
+def test_scales_and_biases_index_formulas():
+    E, Hp, Ip = 1, 1024, 1024
+    nHt, qbH = onl.h_tiling(Hp)
+    nIt, qbI = onl.i_tiling(Ip)
+    s = torch.arange(E * (Hp // 32) * 2 * Ip, dtype=torch.int64).reshape(E, Hp // 32, 2 * Ip)
+    out = onl.tile_gate_up_scale(s).numpy()
+    e, qb, g, ht, f = np.indices(out.shape)
+    it, rest = f // (4 * qbI * 8), f % (4 * qbI * 8)
+    qw, rest = rest // (qbI * 8), rest % (qbI * 8)
+    qbi, qhi = rest // 8, rest % 8
+    j = (((g * nIt + it) * qbI + qbi) * 8 + qhi) * 4 + qw
+    assert np.array_equal(out, s.numpy()[e, ht * qbH + qb, j])
+    b = torch.arange(E * 2 * Ip, dtype=torch.int64).reshape(E, 2 * Ip)
+    out = onl.tile_gate_up_bias(b).numpy()
+    e, f = np.indices(out.shape)
+    qbi, rest = f // (8 * 2 * nIt * 4), f % (8 * 2 * nIt * 4)
+    qhi, rest = rest // (2 * nIt * 4), rest % (2 * nIt * 4)
+    g, rest = rest // (nIt * 4), rest % (nIt * 4)
+    it, qw = rest // 4, rest % 4
+    j = (((g * nIt + it) * qbI + qbi) * 8 + qhi) * 4 + qw
+    assert np.array_equal(out, b.numpy()[e, j])
+    sd = torch.arange(E * (Ip // 32) * Hp, dtype=torch.int64).reshape(E, Ip // 32, Hp)
+    out = onl.tile_down_scale(sd).numpy()
+    e, qbi, it, f = np.indices(out.shape)
+    hb, hn = f // (Hp // 4), f % (Hp // 4)
+    assert np.array_equal(out, sd.numpy()[e, it * qbI + qbi, hn * 4 + hb])
+
+
+@pytest.mark.parametrize("E,H,I,Hp,Ip", [(2, 512, 512, 512, 512), (3, 96, 160, 512, 512),
+                                         (2, 1024, 1536, 1024, 1536), (1, 2880, 2880, 3072, 3072)])
+def test_converter_round_trip_matches_checkpoint_packing(E, H, I, Hp, Ip):
+    from vllm_neuron_amd.neuron_layout import experts_from_neuron_layout
+    from vllm_neuron_amd.weights import MXFP4Experts
+
+    g = torch.Generator().manual_seed(E * 1000 + H + I)
+    gub = torch.randint(0, 256, (E, 2 * I, H // 32, 16), generator=g, dtype=torch.uint8)
+    gus = torch.randint(0, 256, (E, 2 * I, H // 32), generator=g, dtype=torch.uint8)
+    dnb = torch.randint(0, 256, (E, H, I // 32, 16), generator=g, dtype=torch.uint8)
+    dns = torch.randint(0, 256, (E, H, I // 32), generator=g, dtype=torch.uint8)
+    gbias = (torch.randn(E, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    dbias = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    want = MXFP4Experts.from_checkpoint(gub, gus, dnb, dns, gbias, dbias)
+    got = experts_from_neuron_layout(
+        onl.gate_up_blocks(gub, Hp, Ip), onl.gate_up_scales(gus, Hp, Ip),
+        onl.down_blocks(dnb, Hp, Ip), onl.down_scales(dns, Hp, Ip), H, I,
+        gate_up_bias=onl.gate_up_bias(gbias, Ip, 1.0), down_bias=onl.down_bias(dbias, Hp))
+    assert (got.E, got.H, got.I) == (want.E, want.H, want.I)
+    for name in ("gu_q", "gu_s", "dn_q", "dn_s", "gu_bias", "dn_bias"):
+        assert torch.equal(getattr(got, name), getattr(want, name)), name
+
+
+def test_converter_rejects_bad_inputs():
+    from vllm_neuron_amd.neuron_layout import experts_from_neuron_layout
+
+    E, H, I = 1, 512, 512
+    gub = onl.gate_up_blocks(torch.zeros(E, 2 * I, H // 32, 16, dtype=torch.uint8), 512, 512)
+    gus = onl.gate_up_scales(torch.zeros(E, 2 * I, H // 32, dtype=torch.uint8), 512, 512)
+    dnb = onl.down_blocks(torch.zeros(E, H, I // 32, 16, dtype=torch.uint8), 512, 512)
+    dns = onl.down_scales(torch.zeros(E, H, I // 32, dtype=torch.uint8), 512, 512)
+    with pytest.raises(ValueError):
+        experts_from_neuron_layout(gub, gus, dnb, dns, 1024, I)
+    with pytest.raises(TypeError):
+        experts_from_neuron_layout(gub.view(torch.uint8), gus, dnb, dns, H, I)
