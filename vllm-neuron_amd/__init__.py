@@ -6,7 +6,7 @@ expert MLP (moe_cte), decode expert MLP (moe_tkg / moe_block_tkg) and MXFP4
 dequantization, all running hand-written gfx950 HIP kernels from libmxmoe.so.
 """
 
-from . import enums, functional, neuron_layout, weights  # noqa: F401
+from . import checkpoint, enums, functional, neuron_layout, weights  # noqa: F401
 from ._lib import MXMoEError, load_library  # noqa: F401
 
 __version__ = "0.1.0"
