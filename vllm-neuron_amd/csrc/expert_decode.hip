@@ -1,14 +1,17 @@
 // Decode (token generation) expert MLP: weight-streaming grouped GEMMs over the
 // experts the batch selected, fp32 arithmetic as in the reference decode flow.
 //
+//   front end  (mxmoe_moe_decode, T <= 128) router logits split over many workgroups,
+//              then one workgroup for the top-k of every token and the routing below
 //   route      one workgroup: per-expert slot lists (tokens ascending inside an
 //              expert), the list of active experts, per-token slots sorted by expert
 //   gate_up    streaming kernel, one wave per item (active expert, 4 row groups =
 //              2 gate/up pairs): the item's packed weights stream over all of K
 //              through a register ring of D chunks; fused bias, clamps and
 //              activation; the fp32 activation is stored as a bf16 (hi, lo) pair
-//   down       the same streaming kernel over (active expert, 4 row groups of H); two
-//              MFMAs (hi, lo) per product, fp32 bias
+//   down       the same streaming kernel over (active expert, 4 row groups of H, or 8
+//              when enough experts are active to fill the chip with half as many
+//              waves); two MFMAs (hi, lo) per product, fp32 bias
 //   combine    out[t] = bf16(sum over the token's experts in ascending id of y * w)
 // Items are independent and each writes its own outputs.
 #include <math.h>
@@ -35,7 +38,7 @@ __device__ __forceinline__ void tkg_route_block(
   __shared__ int off[kTkgMaxE];
   __shared__ int wsum[16], wact[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < 16 * kTkgMaxE; i += 1024) (&masks[0][0])[i] = 0ull;
+  for (int e = lane; e < E; e += 64) masks[wave][e] = 0ull;  // the rows' first E entries
   __syncthreads();
   int ids[8];
   float vals[8];
@@ -132,20 +135,23 @@ __global__ void __launch_bounds__(1024) tkg_route_kernel(
                   tok_slot, tok_w);
 }
 
-// Decode front end for small batches: router logits with one 16-wave workgroup per
-// 16 x 16 tile, then the top-k of each token (the routing kernel follows).
+// Decode front end for small batches: router logits as 16-token x 16-expert MFMA tiles
+// whose K reduction is split over kFrontSlices workgroups (so the router weights stream
+// through many CUs), then one workgroup that adds the partial sums, takes the top-k of
+// every token and routes the batch.
 constexpr int kFrontMaxT = 128;  // larger batches take the standalone router kernels
+constexpr int kFrontSlices = 4;
+constexpr int kFrontWaves = 16 / kFrontSlices;  // waves per workgroup
 
-// One workgroup (16 waves) per 16-token x 16-expert logits tile: the waves take the
-// 128-wide K chunks round-robin and their partial sums are added in wave order.
-// A = router rows (experts), B = tokens.
-__global__ void __launch_bounds__(1024) front_logits_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ bias,
-                                                            float* __restrict__ logits, int T,
-                                                            int H, int E) {
-  __shared__ f32x4 red[16][64];
+// Wave w of slice s (blockIdx.z) takes the 128-wide K chunks gw, gw + 16, ... with
+// gw = s * kFrontWaves + w; the workgroup adds its waves' sums in wave order and
+// stores partial s [kFrontSlices, T, E].  A = router rows (experts), B = tokens.
+__global__ void __launch_bounds__(64 * kFrontWaves) front_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float* __restrict__ part,
+    int T, int H, int E) {
+  __shared__ f32x4 red[kFrontWaves][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int gw = blockIdx.z * kFrontWaves + wave;
   const int q = lane >> 4, r16 = lane & 15;
   const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
   const int nc = (H + 127) / 128, tail_q = (H % 128) / 32;
@@ -153,7 +159,7 @@ __global__ void __launch_bounds__(1024) front_logits_kernel(const uint16_t* __re
   const uint16_t* wr = w + (size_t)min(e0 + r16, E - 1) * H;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  for (int c = wave; c < nc; c += 16) {
+  for (int c = gw; c < nc; c += 16) {
     const bool ok = (c < H / 128) || (q < tail_q);
     const int k0 = ok ? c * 128 + q * 32 : 0;
     u32x4 xv[4], wv[4];
@@ -170,34 +176,80 @@ __global__ void __launch_bounds__(1024) front_logits_kernel(const uint16_t* __re
   }
   red[wave][lane] = acc;
   __syncthreads();
-  if (tid < 256) {
-    const int l = tid & 63, i = tid >> 6;  // D lane l, element i: expert 4(l/16)+i, token l%16
+  for (int o = tid; o < 256; o += 64 * kFrontWaves) {
+    const int l = o & 63, i = o >> 6;  // D lane l, element i: expert 4(l/16)+i, token l%16
     float v = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < 16; ++wv) v += red[wv][l][i];
+    for (int wv = 0; wv < kFrontWaves; ++wv) v += red[wv][l][i];
     const int tok = t0 + (l & 15), ex = e0 + 4 * (l >> 4) + i;
-    if (tok < T && ex < E) {
-      if (bias) v += bf16_bits_to_f32(bias[ex]);
-      logits[(size_t)tok * E + ex] = v;
-    }
+    if (tok < T && ex < E) part[((size_t)blockIdx.z * T + tok) * E + ex] = v;
   }
 }
 
-// Top-k of every token, one wave per token, four tokens per workgroup.
+// One workgroup of 1024 threads: logits = partials added in slice order + bias (stored
+// to logits), the top-k of token t by the 16-lane row t % 64 (lane j holds experts
+// j, j+16, ...), then the routing of the batch from the selections kept in LDS.
 template <int PER>
-__global__ void __launch_bounds__(256) front_topk_kernel(const float* __restrict__ logits, int T,
-                                                         int E, int K, int act, int act_first,
-                                                         int renorm, float renorm_eps,
-                                                         int32_t* __restrict__ topk_idx,
-                                                         float* __restrict__ topk_val) {
-  const int t = blockIdx.x * 4 + wave_id();
-  if (t >= T) return;
-  float v[PER];
-  load_row_wave<PER>(logits + (size_t)t * E, E, v);
-  int sel_idx[8];
-  float out[8];
-  topk_row_wave<PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
-  store_topk_wave(sel_idx, out, K, topk_idx + (size_t)t * K, topk_val + (size_t)t * K);
+__global__ void __launch_bounds__(1024) front_route_kernel(
+    const float* __restrict__ part, const uint16_t* __restrict__ bias, float* __restrict__ logits,
+    int T, int E, int K, int act, int act_first, int renorm, float renorm_eps, int scale_mode,
+    int32_t* __restrict__ expert_off, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
+    int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot, float* __restrict__ tok_w) {
+  __shared__ int32_t s_idx[kFrontMaxT * 8];
+  __shared__ float s_val[kFrontMaxT * 8];
+  const int tid = threadIdx.x, row = tid >> 4, j = tid & 15;
+  // Every load is issued before any is used (addresses clamped into the row), so the
+  // partial sums and the bias arrive in one round trip.
+  float bv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) bv[i] = 0.f;
+  if (bias) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) bv[i] = bf16_bits_to_f32(bias[min(j + 16 * i, E - 1)]);
+  }
+  for (int t = row; t < T; t += 64) {
+    float pv[kFrontSlices][PER];
+#pragma unroll
+    for (int sl = 0; sl < kFrontSlices; ++sl)
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        pv[sl][i] = part[((size_t)sl * T + t) * E + min(j + 16 * i, E - 1)];
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      float a = pv[0][i];
+#pragma unroll
+      for (int sl = 1; sl < kFrontSlices; ++sl) a += pv[sl][i];
+      a += bv[i];
+      const int e = j + 16 * i;
+      if (e < E) logits[(size_t)t * E + e] = a;
+      v[i] = e < E ? a : -INFINITY;
+    }
+    int sel_idx[8];
+    float out[8];
+    topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+    if (j < K) {
+      int si = 0;
+      float so = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k == j) {
+          si = sel_idx[k];
+          so = out[k];
+        }
+      s_idx[t * K + j] = si;
+      s_val[t * K + j] = so;
+    }
+  }
+  __syncthreads();
+  tkg_route_block(s_idx, s_val, T, K, E, scale_mode, expert_off, active, n_active, slot_tok,
+                  tok_slot, tok_w);
+}
+
+// Experts per lane of a 16-lane row: the template argument of front_route_kernel.
+inline int front_per_lane(int E) {
+  const int per = (E + 15) / 16;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : per <= 16 ? 16 : 32;
 }
 
 __device__ __forceinline__ float clampf_ref(float v, float lo, float hi) {
@@ -232,6 +284,7 @@ struct StreamGeom {
   uint32_t rg_bytes, q_bytes;
   int rv;             // valid row groups in the tile (<= R)
   int nfull, tail_q;  // full 128-wide chunks, 32-blocks in the partial last chunk
+  int cb, ce;         // the K chunks [cb, ce) this tile streams
 };
 
 // Plain loads only, so nothing waits on them before their use: lanes past K in a
@@ -260,8 +313,9 @@ __device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, co
 #pragma unroll
   for (int h = 0; h < R / 4; ++h) {
     const uint32_t qq = 4 * h < g.rv ? h : 0;  // a partial last tile stays in its expert
-    f.s[h] = *reinterpret_cast<const uint32_t*>(g.ws + qq * g.q_bytes + (uint32_t)c * 256u +
-                                                lo * 4u);
+    // Scales are read once per step too (non-temporal, about 2 % faster than cached).
+    f.s[h] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+        g.ws + qq * g.q_bytes + (uint32_t)c * 256u + lo * 4u));
   }
   const uint32_t k0b = ok ? (uint32_t)(c * 128 + q * 32) * 2u : 0u;  // byte offset in a row
 #pragma unroll
@@ -280,8 +334,9 @@ __device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, co
 template <int R, int NT, bool SPLIT>
 __device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int c,
                                           const StreamGeom& g, f32x4 (&acc)[R][NT]) {
-  // chunks at or past nc (the loop rounds up to whole rings) contribute exact zeros
-  const bool ok = (c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q);
+  // chunks at or past ce (the loop rounds up to whole rings) contribute exact zeros
+  const bool ok =
+      c < g.ce && ((c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q));
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float sc = ok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
@@ -299,31 +354,32 @@ __device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int 
   }
 }
 
-// One wave streams an R-row-group tile over all nc K chunks, D chunks in flight.
-// Activation rows are b1 (and, with SPLIT, b2 for the lo parts) plus this lane's
-// byte offset row_off[t] for token tile t (a valid row also for lanes without a token).
+// One wave streams an R-row-group tile over the K chunks [g.cb, g.ce), D chunks in
+// flight.  Activation rows are b1 (and, with SPLIT, b2 for the lo parts) plus this
+// lane's byte offset row_off[t] for token tile t (a valid row also for lanes without a
+// token).
 template <int R, int NT, bool SPLIT, int D>
 __device__ __forceinline__ void stream_tile(const StreamGeom& g, const char* b1, const char* b2,
-                                            const uint32_t* row_off, int nc,
-                                            f32x4 (&acc)[R][NT]) {
+                                            const uint32_t* row_off, f32x4 (&acc)[R][NT]) {
   // Every ring slot is refilled right after its MFMAs, unconditionally (past the
   // end with the last chunk again, a cache hit), and the loop body has no branch:
   // a load whose issue depends on a branch would make the wait before a chunk's
   // MFMAs assume the shorter queue and drain the loads of the chunks behind it, and
   // a branch join around the MFMAs would copy the accumulators.  The loop covers
-  // whole rings; chunks past nc add exact zeros.
+  // whole rings; chunks past ce add exact zeros.
+  const int cl = g.ce > g.cb ? g.ce - 1 : g.cb;  // last chunk to (re)load
   ChunkFrag<R, NT, SPLIT> f[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load_chunk(f[d], d < nc ? d : nc - 1, g, b1, b2, row_off);
+    load_chunk(f[d], g.cb + d < cl ? g.cb + d : cl, g, b1, b2, row_off);
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int c = 0; c < nc; c += D) {
+  for (int c = g.cb; c < g.ce; c += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       mma_chunk(f[d], c + d, g, acc);
       const int cn = c + d + D;
-      load_chunk(f[d], cn < nc ? cn : nc - 1, g, b1, b2, row_off);
+      load_chunk(f[d], cn < cl ? cn : cl, g, b1, b2, row_off);
       // Keep program order: the scheduler would otherwise hoist the refills above
       // the MFMAs and consume them in the same iteration, leaving nothing in flight.
       __builtin_amdgcn_sched_barrier(0);
@@ -367,6 +423,8 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   g.nfull = K / 128;
   g.tail_q = (K % 128) / 32;
   const int ai = item / ipe, ri = item - ai * ipe;
+  g.cb = 0;
+  g.ce = nc;
   // Item metadata is wave-uniform: keep it in scalar registers.
   const int e = __builtin_amdgcn_readfirstlane(a.active[ai]);
   const int rg0 = ri * R;
@@ -392,7 +450,7 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_tile<R, NT, SPLIT, D>(g, b1, b2, row_off, nc, acc);
+    stream_tile<R, NT, SPLIT, D>(g, b1, b2, row_off, acc);
     typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -441,12 +499,14 @@ __host__ __device__ inline int tkg_items_per_expert(int H, int I, bool gate_up, 
   return (n_rg + R - 1) / R;
 }
 
-// Grid dispatch: wave w of workgroup b takes item 4b + w; the grid covers every
-// expert, waves past the active experts' items return at once.
-template <int R, int NT, bool GATE_UP, int D>
-__global__ void __launch_bounds__(256) tkg_stream_kernel(TkgArgs a) {
+// Grid dispatch: wave w of workgroup b takes item WPB * b + w; the grid covers every
+// expert, waves past the active experts' items return at once.  One token tile per
+// item keeps three waves per SIMD (168 registers).
+template <int R, int NT, bool GATE_UP, int D, int WPB>
+__global__ void __launch_bounds__(64 * WPB)
+    __attribute__((amdgpu_waves_per_eu(NT == 1 ? 3 : 1))) tkg_stream_kernel(TkgArgs a) {
   const int ipe = tkg_items_per_expert(a.H, a.I, GATE_UP, R);
-  const int item = blockIdx.x * 4 + wave_id();
+  const int item = blockIdx.x * WPB + (WPB == 1 ? 0 : wave_id());
   if (item >= (*a.n_active) * ipe) return;
   tkg_item<R, NT, GATE_UP, D>(a, item, ipe);
 }
@@ -532,7 +592,7 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
                         const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
                         int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
                         const float* clamps, int scale_mode, uint16_t* out, const TkgWs& w,
-                        void* const* ev, hipStream_t s) {
+                        void* const* ev, hipStream_t s, bool routed = false) {
   TkgArgs a = {};
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
@@ -546,9 +606,10 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
   a.n_active = w.n_active;
   a.slot_tok = w.slot_tok;
   mark_event(ev, 0, s);
-  hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
-                     top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
-                     w.tok_slot, w.tok_w);
+  if (!routed)  // else the decode front end has routed the batch into w
+    hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
+                       top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
+                       w.tok_slot, w.tok_w);
   mark_event(ev, 1, s);
   TkgArgs gu = a, dn = a;
   gu.x = x;
@@ -563,28 +624,37 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
   dn.ws = dn_s;
   dn.bias = dn_bias;
   dn.y = w.y;
-  // One wave per item, four per workgroup; the grid covers every expert (the
-  // active count is known on the device only) and the surplus waves return at once.
-  auto grid = [&](bool gate_up, int R) {
-    return dim3((unsigned)((E * tkg_items_per_expert((int)H, (int)I, gate_up, R) + 3) / 4));
+  // One wave per item; the grid covers every expert (the active count is known on the
+  // device only) and the surplus waves return at once.
+  auto grid = [&](bool gate_up, int R, int wpb) {
+    return dim3((unsigned)((E * tkg_items_per_expert((int)H, (int)I, gate_up, R) + wpb - 1) /
+                           wpb));
   };
-  // Token tiles per pass: an expert with more tokens loops over passes.
-  // down with 8 row groups per item halves its activation loads per weight byte; it
-  // pays off while the item count still fills the GPU (expected active experts
-  // E (1 - (1 - k/E)^T) from the batch size).
-  const double active_est = (double)E * (1.0 - pow(1.0 - (double)top_k / (double)E, (double)T));
-  const bool down8 = active_est * (double)(H / 16) / 8.0 >= 2048.0;
   if (T <= 16 || T * top_k <= 8 * E) {
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
+    // One 16-token tile per expert.
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>), grid(true, 4, 4), dim3(256), 0, s,
+                       gu);
     mark_event(ev, 2, s);
-    if (down8)
-      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 2>), grid(false, 8), dim3(256), 0, s, dn);
+    // down: with enough items (expected active experts E (1 - (1 - k/E)^T) from the batch
+    // size), 8 row groups per item with one chunk in flight, three waves per SIMD, one
+    // wave per workgroup: a 64-token batch's down items then run in one round, spread
+    // over the CUs one wave at a time so that every CU streams about the same share of
+    // the weights.  With few items, 4 row groups and two chunks in flight per wave.
+    const double active_est =
+        (double)E * (1.0 - pow(1.0 - (double)top_k / (double)E, (double)T));
+    if (active_est * (double)tkg_items_per_expert((int)H, (int)I, false, 8) >= 900.0)
+      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 1, 1>), grid(false, 8, 1), dim3(64), 0,
+                         s, dn);
     else
-      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 4>), grid(false, 4, 4), dim3(256), 0,
+                         s, dn);
   } else {
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2>), grid(true, 4), dim3(256), 0, s, gu);
+    // Two token tiles per pass (an expert with more tokens loops over passes).
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2, 4>), grid(true, 4, 4), dim3(256), 0, s,
+                       gu);
     mark_event(ev, 2, s);
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, false, 2>), grid(false, 4), dim3(256), 0, s, dn);
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, false, 2, 4>), grid(false, 4, 4), dim3(256), 0,
+                       s, dn);
   }
   mark_event(ev, 3, s);
   hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
@@ -594,6 +664,7 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
 }
 
 struct DecodeWs {
+  float* part;  // front end: [kFrontSlices, T, E] partial logits (T <= kFrontMaxT)
   float* logits;
   int32_t* idx;
   float* val;
@@ -605,6 +676,7 @@ static size_t decode_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t
                            int K, DecodeWs* d) {
   Carver cv(base, cap);
   DecodeWs r;
+  r.part = cv.take<float>((T <= kFrontMaxT ? T : 0) * kFrontSlices * E);
   r.logits = cv.take<float>(T * E);
   r.idx = cv.take<int32_t>(T * K);
   r.val = cv.take<float>(T * K);
@@ -672,27 +744,31 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
   mark_event(stage_events, 0, s);
   if (T <= kFrontMaxT) {
     hipLaunchKernelGGL(front_logits_kernel,
-                       dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16)), dim3(1024), 0,
-                       s, x, router_w, router_b, logits, (int)T, (int)H, (int)E);
+                       dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16), kFrontSlices),
+                       dim3(64 * kFrontWaves), 0, s, x, router_w, d.part, (int)T, (int)H, (int)E);
     const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
-    const dim3 gt((unsigned)((T + 3) / 4));
-#define MXMOE_FRONT(P)                                                                      \
-  hipLaunchKernelGGL(front_topk_kernel<P>, gt, dim3(256), 0, s, logits, (int)T, (int)E, top_k, \
-                     router_act, af, rn, renorm_eps, d.idx, d.val)
-    switch (topk_per_lane((int)E)) {
+#define MXMOE_FRONT(P)                                                                       \
+  hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b, logits, \
+                     (int)T, (int)E, top_k, router_act, af, rn, renorm_eps, scale_mode,        \
+                     w.expert_off, w.active, w.n_active, w.slot_tok, w.tok_slot, w.tok_w)
+    switch (front_per_lane((int)E)) {
       case 1: MXMOE_FRONT(1); break;
       case 2: MXMOE_FRONT(2); break;
       case 4: MXMOE_FRONT(4); break;
-      default: MXMOE_FRONT(8); break;  // E <= 512 here
+      case 8: MXMOE_FRONT(8); break;
+      case 16: MXMOE_FRONT(16); break;
+      default: MXMOE_FRONT(32); break;  // E <= 512
     }
 #undef MXMOE_FRONT
     rc = check_launch("moe_decode front end");
     if (rc) return rc;
-  } else {
-    rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
-                    renorm_eps, logits, nullptr, d.idx, d.val, s);
-    if (rc) return rc;
+    return tkg_pipeline(x, nullptr, nullptr, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I,
+                        E, top_k, act, clamps, scale_mode, out, w,
+                        stage_events ? stage_events + 1 : nullptr, s, /*routed=*/true);
   }
+  rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
+                  renorm_eps, logits, nullptr, d.idx, d.val, s);
+  if (rc) return rc;
   return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
                       top_k, act, clamps, scale_mode, out, w,
                       stage_events ? stage_events + 1 : nullptr, s);

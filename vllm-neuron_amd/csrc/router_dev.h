@@ -60,6 +60,55 @@ __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
   v = m;
 }
 
+// The same reductions over each row of 16 lanes (the first four DPP moves): every
+// lane of a row ends with its row's result.
+#define MXMOE_ROW_REDUCE(T, OP, V, IDENT)                                                    \
+  do {                                                                                   \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0xB1, 0xf);                                          \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x4E, 0xf);                                          \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x141, 0xf);                                         \
+    MXMOE_DPP_STEP(T, OP, V, IDENT, 0x140, 0xf);                                         \
+  } while (0)
+
+__device__ __forceinline__ float row16_max(float v) {
+  MXMOE_ROW_REDUCE(float, fmax_op, v, -INFINITY);
+  return v;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  MXMOE_ROW_REDUCE(float, fadd_op, v, 0.0f);
+  return v;
+}
+
+__device__ __forceinline__ int row16_min(int v) {
+  MXMOE_ROW_REDUCE(int, imin_op, v, 0x7fffffff);
+  return v;
+}
+
+// wave_argmax over a row of 16 lanes.
+__device__ __forceinline__ void row16_argmax(float& v, int& idx) {
+  const float m = row16_max(v);
+  idx = row16_min(v == m ? idx : 0x7fffffff);
+  v = m;
+}
+
+// Reductions over a group of W lanes (the wave, or a row of 16).
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (W == 64) return wave_max(v);
+  else return row16_max(v);
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (W == 64) return wave_sum(v);
+  else return row16_sum(v);
+}
+template <int W>
+__device__ __forceinline__ void group_argmax(float& v, int& idx) {
+  if constexpr (W == 64) wave_argmax(v, idx);
+  else row16_argmax(v, idx);
+}
+
 // A row of E <= 64*PER logits into one wave: lane l holds experts l, l+64, ...
 template <int PER>
 __device__ __forceinline__ void load_row_wave(const float* __restrict__ row, int E,
@@ -77,11 +126,13 @@ __device__ __forceinline__ void load_row_wave(const float* __restrict__ row, int
 // expert id), then the activation over the k selected values; act_first = 1: the
 // activation over all E logits, then top-k.  renorm divides the k values by (their
 // sum + eps).  Every lane returns the same sel_idx[0..K) and out[0..K).
-template <int PER>
-__device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, int K, int act,
-                                              int act_first, int renorm, float renorm_eps,
-                                              int (&sel_idx)[8], float (&out)[8]) {
-  const int lane = threadIdx.x & 63;
+// topk_row_group<W, PER> does the same for a group of W lanes (W = 64: the wave; W = 16:
+// a row of 16 lanes, lane j of the row holding experts j, j+16, ...).
+template <int W, int PER>
+__device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, int K, int act,
+                                               int act_first, int renorm, float renorm_eps,
+                                               int (&sel_idx)[8], float (&out)[8]) {
+  const int lane = threadIdx.x & (W - 1);
   float score[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) score[i] = vals[i];
@@ -90,20 +141,20 @@ __device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, i
       float m = score[0];
 #pragma unroll
       for (int i = 1; i < PER; ++i) m = fmaxf(m, score[i]);
-      m = wave_max(m);
+      m = group_max<W>(m);
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        score[i] = lane + 64 * i < E ? expf(score[i] - m) : 0.f;
+        score[i] = lane + W * i < E ? expf(score[i] - m) : 0.f;
         s += score[i];
       }
-      s = wave_sum(s);
+      s = group_sum<W>(s);
 #pragma unroll
-      for (int i = 0; i < PER; ++i) score[i] = lane + 64 * i < E ? score[i] / s : -INFINITY;
+      for (int i = 0; i < PER; ++i) score[i] = lane + W * i < E ? score[i] / s : -INFINITY;
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i)
-        score[i] = lane + 64 * i < E ? sigmoid_f32(score[i]) : -INFINITY;
+        score[i] = lane + W * i < E ? sigmoid_f32(score[i]) : -INFINITY;
     }
   }
   // k rounds of arg-max; selected entries are knocked out.
@@ -117,17 +168,17 @@ __device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, i
     int bi = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && (score[i] > bv || (score[i] == bv && e < bi))) {
-        bv = score[i];
-        bi = e;
-      }
+      // bitwise logic: selects, no branch per element
+      const int e = lane + W * i;
+      const bool take = (e < E) & ((score[i] > bv) | ((score[i] == bv) & (e < bi)));
+      bv = take ? score[i] : bv;
+      bi = take ? e : bi;
     }
-    wave_argmax(bv, bi);
+    group_argmax<W>(bv, bi);
     sel_idx[k] = bi;
     sel_val[k] = bv;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) score[i] = (lane + 64 * i == bi) ? -INFINITY : score[i];
+    for (int i = 0; i < PER; ++i) score[i] = (lane + W * i == bi) ? -INFINITY : score[i];
   }
   // Activation over the selected values unless it came first, then optional renorm.
 #pragma unroll
@@ -161,6 +212,13 @@ __device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, i
     for (int k = 0; k < 8; ++k)
       if (k < K) out[k] = out[k] / s;
   }
+}
+
+template <int PER>
+__device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, int K, int act,
+                                              int act_first, int renorm, float renorm_eps,
+                                              int (&sel_idx)[8], float (&out)[8]) {
+  topk_row_group<64, PER>(vals, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
 }
 
 // Values per lane for E experts: the template argument of topk_row_wave.
