@@ -60,7 +60,22 @@ def parse():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time decode with eager launches")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three device copies of exactly 1 GiB (the reference "
+                         "kernel that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_calibration():
+    import torch
+
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": a.numel(), "copies": 3}))
 
 
 def make_layer(E, K, H, I, limit, biases, dev, gen):
@@ -99,16 +114,20 @@ def gate_up_bytes_per_expert(H, I, biases):
     return 2 * I * H // 2 + 2 * I * H // 32 + (2 * I * 2 if biases else 0)
 
 
-def measured_traffic(workload, decode_T):
-    """HBM bytes per launch of the decode gate_up kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) for this workload, else None."""
+def measured_traffic(workload, decode_T, prefill_T):
+    """HBM bytes per launch of the decode gate_up kernel and of the prefill gate_up GEMM,
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) for this
+    workload and batch sizes, else None; and the summary they come from."""
     path = ROOT / "profiles" / f"decode_traffic_{workload}.json"
     if not path.exists():
-        return None, None
+        return None, None, None
     d = json.loads(path.read_text())
-    if d.get("decode_tokens") != decode_T:
-        return None, None
-    return d["traffic_bytes"], d["source"]
+    dec = d["traffic_bytes"] if d.get("decode_tokens") == decode_T else None
+    pre = None
+    if d.get("prefill_tokens") == prefill_T and d.get("prefill_gate_up"):
+        v = next(iter(d["prefill_gate_up"].values()))
+        pre = v["read_bytes"] + v["write_bytes"]
+    return dec, pre, d["source"]
 
 
 def cpu_baseline(wl, decode_T, prefill_T):
@@ -165,6 +184,10 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
               "multi-GPU expert parallelism is not built in this tier.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import torch
 
@@ -265,8 +288,8 @@ def main():
         "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
     }
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    traffic, traffic_src = measured_traffic(args.workload, dT)
-    roofline = {"bound": "hbm", "kernel": "tkg_stream_kernel<4, 1, true, 2> (gate_up)",
+    traffic, traffic_pre, traffic_src = measured_traffic(args.workload, dT, pT)
+    roofline = {"bound": "hbm", "kernel": "tkg_stream_kernel<4, 1, true, 2, 4> (gate_up)",
                 "achieved": gu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": gu_gbs / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic_bytes_per_launch": gu_bytes, "avg_launch_ms": gu_ms}
@@ -307,7 +330,8 @@ def main():
             "roofline": {"bound": "mfma", "kernel": "prefill_gemm_kernel<gate_up>",
                          "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": gu_tf / BF16_PEAK_TFLOPS,
-                         "frac_of_mxfp4_peak": gu_tf / MXFP4_PEAK_TFLOPS, "traffic": None,
+                         "frac_of_mxfp4_peak": gu_tf / MXFP4_PEAK_TFLOPS,
+                         "traffic": traffic_pre, "traffic_source": traffic_src,
                          "algorithmic_flops_per_launch": gu_flops, "avg_launch_ms": gu_ms_p},
         }
 

@@ -198,15 +198,13 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
   __shared__ int32_t s_idx[kFrontMaxT * 8];
   __shared__ float s_val[kFrontMaxT * 8];
   const int tid = threadIdx.x, row = tid >> 4, j = tid & 15;
-  // Every load is issued before any is used (addresses clamped into the row), so the
-  // partial sums and the bias arrive in one round trip.
-  float bv[PER];
+  // Every load of a token is issued before any is used (addresses clamped into the row,
+  // the bias read from a valid address also when there is none), so the partial sums
+  // and the bias arrive in one round trip.
+  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(part);
+  uint16_t braw[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) bv[i] = 0.f;
-  if (bias) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) bv[i] = bf16_bits_to_f32(bias[min(j + 16 * i, E - 1)]);
-  }
+  for (int i = 0; i < PER; ++i) braw[i] = bsrc[min(j + 16 * i, E - 1)];
   for (int t = row; t < T; t += 64) {
     float pv[kFrontSlices][PER];
 #pragma unroll
@@ -220,7 +218,7 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
       float a = pv[0][i];
 #pragma unroll
       for (int sl = 1; sl < kFrontSlices; ++sl) a += pv[sl][i];
-      a += bv[i];
+      a += bias ? bf16_bits_to_f32(braw[i]) : 0.f;
       const int e = j + 16 * i;
       if (e < E) logits[(size_t)t * E + e] = a;
       v[i] = e < E ? a : -INFINITY;

@@ -30,7 +30,6 @@ constexpr int kMaxEPerLane = 16;  // E <= 1024
 
 __device__ __forceinline__ float fmax_op(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ float fadd_op(float a, float b) { return a + b; }
-__device__ __forceinline__ int imin_op(int a, int b) { return a < b ? a : b; }
 
 __device__ __forceinline__ float wave_max(float v) {
   MXMOE_WAVE_REDUCE(float, fmax_op, v, -INFINITY);
@@ -40,24 +39,6 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) {
   MXMOE_WAVE_REDUCE(float, fadd_op, v, 0.0f);
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-__device__ __forceinline__ int wave_min(int v) {
-  MXMOE_WAVE_REDUCE(int, imin_op, v, 0x7fffffff);
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
-// Larger value wins; equal values pick the lower index.  A NaN value never wins (fmaxf
-// drops it and NaN == m is false); every lane gets the winner.  When one lane holds the
-// maximum its index is read directly; ties across lanes take a min-reduction.
-__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-  const float m = wave_max(v);
-  const unsigned long long at = __ballot(v == m);
-  if (__popcll(at) == 1)
-    idx = __builtin_amdgcn_readlane(idx, __ffsll((long long)at) - 1);
-  else
-    idx = wave_min(v == m ? idx : 0x7fffffff);
-  v = m;
 }
 
 // The same reductions over each row of 16 lanes (the first four DPP moves): every
@@ -80,18 +61,6 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ int row16_min(int v) {
-  MXMOE_ROW_REDUCE(int, imin_op, v, 0x7fffffff);
-  return v;
-}
-
-// wave_argmax over a row of 16 lanes.
-__device__ __forceinline__ void row16_argmax(float& v, int& idx) {
-  const float m = row16_max(v);
-  idx = row16_min(v == m ? idx : 0x7fffffff);
-  v = m;
-}
-
 // Reductions over a group of W lanes (the wave, or a row of 16).
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
@@ -103,10 +72,49 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (W == 64) return wave_sum(v);
   else return row16_sum(v);
 }
+
+// Max of 64-bit keys over a group of W lanes (row moves, then for W = 64 the row
+// broadcasts and lane 63); lanes a move has no source for keep key 0.
 template <int W>
-__device__ __forceinline__ void group_argmax(float& v, int& idx) {
-  if constexpr (W == 64) wave_argmax(v, idx);
-  else row16_argmax(v, idx);
+__device__ __forceinline__ uint64_t group_max_key(uint64_t v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#define MXMOE_KEY_STEP(CTRL, ROWS)                                                        \
+  {                                                                                       \
+    const uint32_t l2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, ROWS, 0xf, false); \
+    const uint32_t h2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, ROWS, 0xf, false); \
+    const uint64_t a = ((uint64_t)hi << 32) | lo, b = ((uint64_t)h2 << 32) | l2;            \
+    const uint64_t m = b > a ? b : a;                                                     \
+    lo = (uint32_t)m;                                                                     \
+    hi = (uint32_t)(m >> 32);                                                             \
+  }
+  MXMOE_KEY_STEP(0xB1, 0xf)
+  MXMOE_KEY_STEP(0x4E, 0xf)
+  MXMOE_KEY_STEP(0x141, 0xf)
+  MXMOE_KEY_STEP(0x140, 0xf)
+  if constexpr (W == 64) {
+    MXMOE_KEY_STEP(0x142, 0xa)
+    MXMOE_KEY_STEP(0x143, 0xc)
+    lo = (uint32_t)__builtin_amdgcn_readlane((int)lo, 63);
+    hi = (uint32_t)__builtin_amdgcn_readlane((int)hi, 63);
+  }
+#undef MXMOE_KEY_STEP
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Selection key of (score, expert e): the score's bits mapped to an unsigned order
+// (larger score, larger key; -0 counts as +0) in the high word and ~e in the low word,
+// so the largest key is the largest score with the lowest expert id.  NaN scores and
+// experts past E get key 0 and are never selected.
+__device__ __forceinline__ uint64_t topk_key(float v, int e, int E) {
+  const uint32_t b = __float_as_uint(v + 0.0f);
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  const uint64_t k = ((uint64_t)o << 32) | (uint32_t)~e;
+  return (e < E && !(v != v)) ? k : 0ull;
+}
+
+__device__ __forceinline__ float topk_key_value(uint64_t k) {
+  const uint32_t o = (uint32_t)(k >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
 // A row of E <= 64*PER logits into one wave: lane l holds experts l, l+64, ...
@@ -157,28 +165,26 @@ __device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, 
         score[i] = lane + W * i < E ? sigmoid_f32(score[i]) : -INFINITY;
     }
   }
-  // k rounds of arg-max; selected entries are knocked out.
+  // k rounds of arg-max over the selection keys (descending score, equal scores ->
+  // lower expert id); selected keys are knocked out.  With no candidate left a round
+  // yields index 0x7fffffff and value -inf.
+  uint64_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) key[i] = topk_key(score[i], lane + W * i, E);
   float sel_val[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     sel_idx[k] = 0;
     sel_val[k] = 0.f;
     if (k >= K) continue;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint64_t best = key[0];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      // bitwise logic: selects, no branch per element
-      const int e = lane + W * i;
-      const bool take = (e < E) & ((score[i] > bv) | ((score[i] == bv) & (e < bi)));
-      bv = take ? score[i] : bv;
-      bi = take ? e : bi;
-    }
-    group_argmax<W>(bv, bi);
-    sel_idx[k] = bi;
-    sel_val[k] = bv;
+    for (int i = 1; i < PER; ++i) best = key[i] > best ? key[i] : best;
+    best = group_max_key<W>(best);
+    sel_idx[k] = best ? (int)~(uint32_t)best : 0x7fffffff;
+    sel_val[k] = best ? topk_key_value(best) : -INFINITY;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) score[i] = (lane + W * i == bi) ? -INFINITY : score[i];
+    for (int i = 0; i < PER; ++i) key[i] = key[i] == best ? 0ull : key[i];
   }
   // Activation over the selected values unless it came first, then optional renorm.
 #pragma unroll
