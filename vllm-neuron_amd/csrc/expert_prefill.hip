@@ -1,19 +1,23 @@
 // Prefill (context encoding) expert MLP over the blockwise mapping.
 //
-// Both projections run the same LDS-tiled grouped GEMM:
-//   workgroup tile = 128 slots (M) x 512 weight rows (N, 32 row groups) x 128-wide
-//   K chunks; 8 waves as 2 (M) x 4 (N), each wave 64 slots x 128 rows = 8 x 4
-//   MFMA 16x16x32 tiles.  Per chunk the workgroup moves 32 KiB of activations (bf16,
-//   16-byte blocks XOR-swizzled by row against bank conflicts), 32 KiB of packed
-//   weights and 2 KiB of scales from global memory straight into LDS (no register
-//   staging), two stages deep: chunk c + 1 streams in while chunk c computes.
-//   Weights are dequantized from LDS to bf16 in registers by the CDNA4 scaled
-//   conversion, right before the MFMAs.
-//   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one
-//   expert; tiles whose 128 slots are all padding exit at once, and inside a tile
-//   each wave runs only the 16-slot MFMA tiles that hold real slots.  Tiles are
-//   ordered N-fastest and dealt out XCD by XCD, so the workgroups sharing an
-//   M-tile's activations (and an expert's weights) sit on the same L2.
+// Both projections run the same grouped GEMM:
+//   workgroup tile = 128 slots (M) x 512 weight rows (N, 32 row groups) over all of K in
+//   128-wide chunks; 8 waves, wave w owns row groups 4w..4w+3 (64 rows = 2 gate/up
+//   pairs) against all 128 slots (up to 8 MFMA 16x16x32 tiles of 16 slots).
+//   Weights bypass LDS: each wave streams its own rows global -> registers through a
+//   ring of two chunks (the packed layout is MFMA operand order) and dequantizes them
+//   once, with the CDNA4 scaled conversion, right before its MFMAs.
+//   Activations are shared: the 128 slots' rows of a chunk (32 KiB of bf16, 16-byte
+//   blocks XOR-swizzled by row against bank conflicts) go global -> LDS by direct
+//   loads into a ring of four stages, three chunks ahead.  One s_barrier per chunk,
+//   preceded by a wait for the wave's own direct loads of the chunk about to be read
+//   only (a counted vmcnt, not the full drain of __syncthreads), keeps the weight and
+//   activation streams in flight across chunks.
+//   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one expert;
+//   tiles whose 128 slots are all padding exit at once, and the waves run only the
+//   16-slot tiles up to the last one holding a real slot (rounded to 1, 2, 4 or 8).
+//   Tiles are ordered N-fastest and dealt out XCD by XCD, so the workgroups sharing an
+//   M-tile's activations sit on the same L2.
 // gate_up: A = x rows gathered through token_position_to_id; epilogue = bias,
 //          clamps, activation and up * act with the reference's bf16 roundings;
 //          writes h [slots, I] bf16.
@@ -29,9 +33,11 @@
 
 namespace mxmoe {
 
-constexpr int kPM = 128;    // slots per M-tile
-constexpr int kPRG = 32;    // row groups per N-tile (512 rows), 8 per wave
-constexpr int kPThreads = 512;
+constexpr int kPM = 128;      // slots per M-tile
+constexpr int kPRG = 32;      // row groups per N-tile (512 rows), 4 per wave
+constexpr int kPWaves = 8;
+constexpr int kPThreads = 64 * kPWaves;
+constexpr int kPStages = 4;   // activation chunks in LDS
 
 struct PrefillArgs {
   const uint16_t* a;      // x [T, H] (gate_up) or h [slots, I] (down)
@@ -65,191 +71,218 @@ __device__ __forceinline__ float act_bf16(float g, int act) {
   return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
 }
 
-template <bool GATE_UP>
-__global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs args) {
-  constexpr int WR = kPRG / 4;  // row groups per wave (4 waves across N)
-  constexpr int NQ = kPRG / 4;  // scale quads per tile
-  static_assert(NQ == kPThreads / 64, "one scale quad per wave");
-  // The two pipeline stages are separate arrays indexed at compile time: the
-  // compiler then tells the stage being read from the one a direct load is filling
-  // and waits only for the former.
-  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256];
-  __shared__ __attribute__((aligned(1024))) uint8_t sb0[kPRG * 1024], sb1[kPRG * 1024];
-  __shared__ __attribute__((aligned(1024))) uint8_t ss0[NQ * 256], ss1[NQ * 256];
-  __shared__ int32_t stok[kPM];
-  __shared__ int s_any;
+// Per-workgroup and per-wave constants of a tile.
+struct PrefillTile {
+  const char* a;             // activations
+  uint32_t a_off[4];         // byte offsets of this lane's four source rows (padding: a real row)
+  const uint8_t* wq;         // this wave's first row group
+  const uint8_t* ws;         // this wave's scale quad
+  uint32_t rg_bytes;
+  int rv;                    // valid row groups of this wave (<= 4)
+  int K, nc, nfull, tail_q;
+};
 
-  // XCD-aware tile order (workgroups are dealt round-robin over the 8 XCDs).
-  const int G = args.n_mtiles * args.n_ntiles;
-  const int wg = blockIdx.x;
-  const int xcd = wg & 7, i8 = wg >> 3;
-  const int per = G >> 3, rem = G & 7;
-  const int lin = xcd * per + min(xcd, rem) + i8;
-  const int mt = lin / args.n_ntiles, nt = lin % args.n_ntiles;
-  const int m0 = mt * kPM;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int q = lane >> 4;
+// One weight chunk of a wave in registers: 4 row groups x 16 B per lane, and the
+// 32-bit scale word of its quad.
+struct PrefillB {
+  u32x4 w[4];
+  uint32_t s;
+};
 
-  if (tid == 0) s_any = 0;
-  __syncthreads();
-  if (tid < kPM) {
-    // Without a mapping (plain linear) slot m0 + tid is row m0 + tid of A.
-    int tk = args.tp2id ? args.tp2id[m0 + tid] : m0 + tid;
-    if (tk < 0 || tk >= args.T) tk = -1;
-    stok[tid] = tk;
-    if (tk >= 0) s_any = 1;
-  }
-  __syncthreads();
-  if (!s_any) return;
+// The activation stages are separate arrays of the kernel, chosen at compile time by a
+// selector (stage(std::integral_constant<int, S>())): the compiler then tells the stage
+// being read from the ones direct loads are filling; through a pointer, or with arrays
+// shared by several kernels, it could not and would drain every load before each LDS
+// read.
+template <int S>
+using StageC = std::integral_constant<int, S>;
 
-  const int e = args.b2e ? args.b2e[m0 / args.B] : 0;
-  const int K = args.K;
-  const size_t rg_bytes = (size_t)K * 8, q_sbytes = (size_t)K * 2;
-  const int n_rg_total = args.N_rows / 16;
-  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds NQ scale quads
-  const int rg_valid = min(kPRG, n_rg_total - rg0);
-  const uint8_t* wq = args.wq + ((size_t)e * n_rg_total + rg0) * rg_bytes;
-  const uint8_t* ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rg0 / 4) * q_sbytes;
-  const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
-  auto lane_in_k = [&](int c, int l) { return c < nfull || (l >> 4) < tail_q; };
-
-  // ---- global -> LDS, no registers: each wave issues 4 x 1 KiB of activations (rows
-  // 16w + 4i + lane/16), 4 x 1 KiB of weights (row groups 4w + i) and 256 B of
-  // scales (quad w) per chunk.  A chunk row of activations (128 bf16) is 16 blocks of
-  // 16 B; block cb of row r sits at slot cb ^ (r % 16), so the 16 rows an MFMA reads
-  // hit 16 different slots (no bank conflicts) without padding.  Addresses are
-  // clamped to real data (padding slots read token 0, columns past K read column 0,
-  // row groups past the tile read the first): an MFMA output column depends on its
-  // own slot only and discarded rows are never stored, and compute() gives lanes past
-  // K a zero scale so their weights add nothing.
-  const uint16_t* a_row[4];
-  int a_swz[4];
+// Direct loads of chunk c's activations into LDS: wave w brings rows 16w .. 16w + 15,
+// 4 x 1 KiB (rows 16w + 4i + lane / 16).  The lane's LDS slot (lane % 16) of row r holds
+// column block (lane % 16) ^ (r % 16); columns past K read column 0 of the row.  Issued
+// from inline assembly (M0 = the 1 KiB's LDS address, 16 B per lane): the compiler then
+// keeps no account of them, which it could only settle, across the loop, with a full
+// drain before the stage's first LDS read; the counted barrier waits for them instead.
+__device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 4 * i + (lane >> 4);
-    const int tk = stok[row];
-    a_row[i] = GATE_UP ? args.a + (size_t)(tk >= 0 ? tk : 0) * K
-                       : args.a + (size_t)(m0 + row) * K;
-    a_swz[i] = (lane & 15) ^ (row & 15);  // the column block this lane's slot holds
+    const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
+    const int kcol = c * 128 + swz * 8;
+    const uint32_t off = p.a_off[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
+    const char* src = p.a + off;
+    uint8_t* dst = sa + (16 * wave + 4 * i) * 256;
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+                 : "memory", "m0");
   }
-  auto issue_chunk = [&](auto st_c, int c) {
-    constexpr int ST = decltype(st_c)::value;
-    uint8_t* sa = ST ? sa1 : sa0;
-    uint8_t* sb = ST ? sb1 : sb0;
-    uint8_t* ss = ST ? ss1 : ss0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kcol = c * 128 + a_swz[i] * 8;
-      const uint16_t* src = a_row[i] + (kcol < K ? kcol : 0);  // column 0: in the row
-      __builtin_amdgcn_global_load_lds(src, &sa[(16 * wave + 4 * i) * 256], 16, 0, 0);
-    }
-    const int bl = lane_in_k(c, lane) ? lane : 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rg = 4 * wave + i;
-      const int rgc = rg < rg_valid ? rg : 0;
-      __builtin_amdgcn_global_load_lds(wq + rgc * rg_bytes + (size_t)c * 1024 + bl * 16,
-                                       &sb[rg * 1024], 16, 0, 0);
-    }
-    const int qc = 4 * wave < rg_valid ? wave : 0;
-    __builtin_amdgcn_global_load_lds(ws + qc * q_sbytes + (size_t)c * 256 + bl * 4,
-                                     &ss[wave * 256], 4, 0, 0);
-  };
+}
 
-  const int wm = wave & 1, wn = wave >> 1;
-  // Wave-uniform activity: its row groups exist; ntv = its 16-slot MFMA tiles that
-  // hold a real slot (real slots of a block come first, so they are a prefix).
-  const bool wave_rows = (WR * wn) < rg_valid;
-  int ntv = 0;
+// The wave's weights and scales of chunk c (lanes past K re-read lane 0's bytes of the
+// chunk, row groups past the tile re-read its last valid one), 5 loads.  They are issued
+// from inline assembly, so the compiler does not track them: with direct-to-LDS loads
+// in flight as well it cannot count the wait for register loads and would drain every
+// load (s_waitcnt vmcnt(0)) before their first use.  The compiler takes the outputs as
+// written by the asm statement, while the hardware writes them later: every slot's
+// registers must therefore stay operands of a later wait (prefill_wait_b before use,
+// the loop's final drain for the last, unused refills), or the compiler could hand a
+// register still being loaded to another value.
+__device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p, int c) {
+  const int lane = threadIdx.x & 63;
+  const bool ok = (c < p.nfull) || ((lane >> 4) < p.tail_q);
+  const uint32_t lo = ok ? (uint32_t)lane : 0u;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    bool any = false;
-    for (int i = 0; i < 16; ++i) any |= stok[64 * wm + 16 * t + i] >= 0;
-    ntv = any ? t + 1 : ntv;
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t rr = r < p.rv ? r : p.rv - 1;
+    const uint8_t* src = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u + lo * 16u;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(f.w[r]) : "v"(src) : "memory");
   }
-  const bool active = wave_rows && ntv > 0;
+  const uint8_t* ssrc = p.ws + (uint32_t)c * 256u + lo * 4u;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(f.s) : "v"(ssrc) : "memory");
+}
 
-  f32x4 acc[WR][4];
-#pragma unroll
-  for (int r = 0; r < WR; ++r)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+// Waits until at most N vector memory operations issued after slot f's loads are
+// outstanding (loads retire in issue order); the registers are operands, so no use of
+// them moves above the wait.
+template <int N>
+__device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%5)"
+               : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.s)
+               : "n"(N)
+               : "memory");
+}
 
-  // A wave computes 64 slots (NTV tiles of 16 hold real ones) x WR row groups.
-  auto compute = [&](auto ntv_c, auto st_c, int c) {
-    constexpr int NTV = decltype(ntv_c)::value;
-    constexpr int ST = decltype(st_c)::value;
-    const uint8_t* sa = ST ? sa1 : sa0;
-    const uint8_t* sb = ST ? sb1 : sb0;
-    const uint8_t* ss = ST ? ss1 : ss0;
-    const bool kok = lane_in_k(c, lane);
-    float sc[WR];
+// acc[r][t] += W[row group r] x A[16-slot tile t] over chunk c.  Lanes past K get a zero
+// scale, so their weights add exact zeros.
+template <int NT>
+__device__ __forceinline__ void prefill_compute(const uint8_t* sa, const PrefillB& f,
+                                                const PrefillTile& p, int c,
+                                                f32x4 (&acc)[4][NT]) {
+  const int lane = threadIdx.x & 63, q = lane >> 4;
+  const bool kok = (c < p.nfull) || (q < p.tail_q);
+  float sc[4];
 #pragma unroll
-    for (int h = 0; h < WR / 4; ++h) {
-      const uint32_t s4 =
-          *reinterpret_cast<const uint32_t*>(&ss[(WR / 4 * wn + h) * 256 + lane * 4]);
+  for (int r = 0; r < 4; ++r) sc[r] = kok ? e8m0_to_f32((f.s >> (8 * r)) & 0xffu) : 0.0f;
+  // Per 32-wide step: the four row groups' weights dequantized once, then one
+  // activation fragment at a time against them (few registers live).
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sc[4 * h + r] = kok ? e8m0_to_f32((s4 >> (8 * r)) & 0xffu) : 0.0f;
+  for (int j = 0; j < 4; ++j) {
+    const int blk = (4 * q + j) ^ (lane & 15);
+    bf16x8 wf[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 xv =
+          *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int slot = (4 * q + j) ^ (lane & 15);
-      u32x4 xv[NTV];
-#pragma unroll
-      for (int t = 0; t < NTV; ++t)
-        xv[t] = *reinterpret_cast<const u32x4*>(
-            &sa[(64 * wm + 16 * t + (lane & 15)) * 256 + slot * 16]);
-      // dword j of each row group's 16 bytes: 8 weights of this MFMA step
-      uint32_t wj[WR];
-#pragma unroll
-      for (int r = 0; r < WR; ++r)
-        wj[r] = *reinterpret_cast<const uint32_t*>(&sb[(WR * wn + r) * 1024 + lane * 16 + 4 * j]);
-#pragma unroll
-      for (int r = 0; r < WR; ++r) {
-        const bf16x8 wf = dequant8(wj[r], sc[r]);
-#pragma unroll
-        for (int t = 0; t < NTV; ++t) acc[r][t] = mfma16(wf, as_bf16x8(xv[t]), acc[r][t]);
-      }
-    }
-  };
-  // The whole K loop per tile count, so no branch sits between the MFMAs.  Chunk
-  // c + 1 streams into the other LDS stage while chunk c computes; the barrier at
-  // the top of each half waits (its release fence) for the chunk about to be read
-  // and for every wave to be done with the stage about to be refilled.
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  auto main_loop = [&](auto ntv_c) {
-    issue_chunk(S0(), 0);
-    for (int c = 0; c < nc; c += 2) {
-      __syncthreads();
-      if (c + 1 < nc) issue_chunk(S1(), c + 1);
-      if (active) compute(ntv_c, S0(), c);
-      if (c + 1 >= nc) break;
-      __syncthreads();
-      if (c + 2 < nc) issue_chunk(S0(), c + 2);
-      if (active) compute(ntv_c, S1(), c + 1);
-    }
-  };
-  switch (ntv) {
-    case 1: main_loop(std::integral_constant<int, 1>()); break;
-    case 2: main_loop(std::integral_constant<int, 2>()); break;
-    case 3: main_loop(std::integral_constant<int, 3>()); break;
-    default: main_loop(std::integral_constant<int, 4>()); break;
   }
-  if (!active) return;
+}
 
+// Waits until at most N vector memory operations of this wave are outstanding (loads
+// retire in issue order), then for its LDS operations, then meets the other waves.
+// Unlike __syncthreads() it does not drain the loads issued for later chunks.
+template <int N>
+__device__ __forceinline__ void prefill_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// One chunk: chunk c is in stage S.  Issue order (the vmcnt arithmetic depends on it):
+// prologue: weights of chunks 0 and 1 (2 x 5), direct loads of chunks 0, 1, 2 (3 x 4);
+// step c: [barrier] direct loads of chunk c + 3 (4), [wait] the MFMAs of chunk c, the
+// weights of chunk c + 2 (5).
+//  - barrier: chunk c's direct loads have landed once at most 8 later loads are
+//    outstanding at step 0 and 13 at later steps (exactly 13 at step 1, more later:
+//    the wait then also covers loads two or more steps old);
+//  - weights of chunk c: at most 13 later loads outstanding (exactly 13 from step 2 on;
+//    steps 0 and 1 wait a little longer, once).
+template <int S, int NT, bool ACTIVE, bool FIRST, typename Stage>
+__device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
+                                             const PrefillTile& p, int c, f32x4 (&acc)[4][NT]) {
+  prefill_barrier<(FIRST || !ACTIVE) ? 8 : 13>();
+  prefill_dma(stage(StageC<(S + 3) % kPStages>()), p, min(c + 3, p.nc - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ACTIVE) {
+    prefill_wait_b<13>(f[S % 2]);
+    prefill_compute<NT>(stage(StageC<S>()), f[S % 2], p, c, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    prefill_load_b(f[S % 2], p, min(c + 2, p.nc - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int NT, bool ACTIVE, typename Stage>
+__device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTile& p,
+                                             f32x4 (&acc)[4][NT]) {
+  PrefillB f[2];
+  if constexpr (ACTIVE) {
+    prefill_load_b(f[0], p, 0);
+    prefill_load_b(f[1], p, min(1, p.nc - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  prefill_dma(stage(StageC<0>()), p, 0);
+  prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1));
+  prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  prefill_step<0, NT, ACTIVE, true>(stage, f, p, 0, acc);
+  int c = 1;
+  for (; c + 4 <= p.nc; c += 4) {
+    prefill_step<1, NT, ACTIVE, false>(stage, f, p, c, acc);
+    prefill_step<2, NT, ACTIVE, false>(stage, f, p, c + 1, acc);
+    prefill_step<3, NT, ACTIVE, false>(stage, f, p, c + 2, acc);
+    prefill_step<0, NT, ACTIVE, false>(stage, f, p, c + 3, acc);
+  }
+  if (c < p.nc) {
+    prefill_step<1, NT, ACTIVE, false>(stage, f, p, c, acc);
+    if (c + 1 < p.nc) {
+      prefill_step<2, NT, ACTIVE, false>(stage, f, p, c + 1, acc);
+      if (c + 2 < p.nc) prefill_step<3, NT, ACTIVE, false>(stage, f, p, c + 2, acc);
+    }
+  }
+  // The loads issued past the last chunk (clamped re-loads) land before the wave goes
+  // on: no direct load may still write into LDS once the workgroup is done with it, and
+  // the ring's registers are operands here, so the compiler keeps them allocated until
+  // their last (unused) loads have written them.
+  if constexpr (ACTIVE) {
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(f[0].w[0]), "+v"(f[0].w[1]), "+v"(f[0].w[2]), "+v"(f[0].w[3]),
+                   "+v"(f[0].s), "+v"(f[1].w[0]), "+v"(f[1].w[1]), "+v"(f[1].w[2]),
+                   "+v"(f[1].w[3]), "+v"(f[1].s)
+                 :
+                 : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
+template <bool GATE_UP, int NT, typename Stage>
+__device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArgs& args,
+                                            const PrefillTile& p, const int32_t* stok, int m0,
+                                            int e, int rg_first) {
+  f32x4 acc[4][NT];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  prefill_loop<NT, true>(stage, p, acc);
+
+  const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
   if (GATE_UP) {
     const int I = args.I;
 #pragma unroll
-    for (int pp = 0; pp < WR / 2; ++pp) {
-      if (WR * wn + 2 * pp >= rg_valid) continue;
-      const int P = (rg0 + WR * wn) / 2 + pp;  // pair index = 16 intermediate columns
+    for (int pp = 0; pp < 2; ++pp) {
+      if (2 * pp >= p.rv) continue;
+      const int P = rg_first / 2 + pp;  // pair index = 16 intermediate columns
       const int col0 = 16 * P + 4 * q;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int row = 64 * wm + 16 * t + (lane & 15);
+      for (int t = 0; t < NT; ++t) {
+        const int row = 16 * t + (lane & 15);
         if (stok[row] < 0) continue;
         const f32x4 g4 = acc[2 * pp][t], u4 = acc[2 * pp + 1][t];
         uint16_t h[4];
@@ -271,12 +304,12 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   } else {
     const int H = args.H;
 #pragma unroll
-    for (int r = 0; r < WR; ++r) {
-      if (WR * wn + r >= rg_valid) continue;
-      const int n0 = 16 * (rg0 + WR * wn + r) + 4 * q;
+    for (int r = 0; r < 4; ++r) {
+      if (r >= p.rv) continue;
+      const int n0 = 16 * (rg_first + r) + 4 * q;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int row = 64 * wm + 16 * t + (lane & 15);
+      for (int t = 0; t < NT; ++t) {
+        const int row = 16 * t + (lane & 15);
         if (stok[row] < 0) continue;
         uint16_t y[4];
 #pragma unroll
@@ -290,6 +323,86 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
       }
     }
   }
+}
+
+template <bool GATE_UP>
+__global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs args) {
+  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
+      sa2[kPM * 256], sa3[kPM * 256];
+  __shared__ int32_t stok[kPM];
+  __shared__ int s_last;
+  auto stage = [&](auto s_c) -> uint8_t* {
+    constexpr int S = decltype(s_c)::value;
+    if constexpr (S == 0) return sa0;
+    else if constexpr (S == 1) return sa1;
+    else if constexpr (S == 2) return sa2;
+    else return sa3;
+  };  // last slot of the tile holding a real token, -1 if none
+
+  // XCD-aware tile order (workgroups are dealt round-robin over the 8 XCDs).
+  const int G = args.n_mtiles * args.n_ntiles;
+  const int wg = blockIdx.x;
+  const int xcd = wg & 7, i8 = wg >> 3;
+  const int per = G >> 3, rem = G & 7;
+  const int lin = xcd * per + min(xcd, rem) + i8;
+  const int mt = lin / args.n_ntiles, nt = lin % args.n_ntiles;
+  const int m0 = mt * kPM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+
+  if (tid == 0) s_last = -1;
+  __syncthreads();
+  if (tid < kPM) {
+    // Without a mapping (plain linear) slot m0 + tid is row m0 + tid of A, real below T.
+    int tk = args.tp2id ? args.tp2id[m0 + tid] : (m0 + tid < args.T ? m0 + tid : -1);
+    if (tk < 0 || tk >= args.T) tk = -1;
+    stok[tid] = tk;
+    if (tk >= 0) atomicMax(&s_last, tid);
+  }
+  __syncthreads();
+  const int last = s_last;
+  if (last < 0) return;
+
+  PrefillTile p;
+  const int e = args.b2e ? args.b2e[m0 / args.B] : 0;
+  p.K = args.K;
+  p.rg_bytes = (uint32_t)p.K * 8u;
+  const int n_rg_total = args.N_rows / 16;
+  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds whole scale quads
+  const int rg_valid = min(kPRG, n_rg_total - rg0);
+  const int rg_first = rg0 + 4 * wave;
+  p.rv = min(4, rg_valid - 4 * wave);
+  const int rgw = p.rv > 0 ? rg_first : rg0;  // waves without rows point at valid data
+  p.wq = args.wq + ((size_t)e * n_rg_total + rgw) * p.rg_bytes;
+  p.ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rgw / 4) * (size_t)(2 * p.K);
+  p.nc = (p.K + 127) / 128;
+  p.nfull = p.K / 128;
+  p.tail_q = (p.K % 128) / 32;
+  p.a = reinterpret_cast<const char*>(args.a);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int tk = stok[row];
+    // Padding slots read a real row (token 0 / the tile's first slot): an MFMA output
+    // column depends on its own slot only, and padding columns are never stored.
+    const uint32_t arow = GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + row : m0);
+    p.a_off[i] = arow * (uint32_t)p.K * 2u;
+  }
+  if (p.rv <= 0) {
+    // No row groups in this tile for this wave: it still brings its share of the
+    // activations and meets the barriers.
+    f32x4 none[4][1];
+    prefill_loop<1, false>(stage, p, none);
+    return;
+  }
+  const int ntiles = last / 16 + 1;  // real slots of a block come first
+  if (ntiles <= 1)
+    prefill_run<GATE_UP, 1>(stage, args, p, stok, m0, e, rg_first);
+  else if (ntiles <= 2)
+    prefill_run<GATE_UP, 2>(stage, args, p, stok, m0, e, rg_first);
+  else if (ntiles <= 4)
+    prefill_run<GATE_UP, 4>(stage, args, p, stok, m0, e, rg_first);
+  else
+    prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
 }
 
 // inv[t, e] = slot of (t, e) or -1.
