@@ -16,8 +16,15 @@
 //   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one expert;
 //   tiles whose 128 slots are all padding exit at once, and the waves run only the
 //   16-slot tiles up to the last one holding a real slot (rounded to 1, 2, 4 or 8).
-//   Tiles are ordered N-fastest and dealt out XCD by XCD, so the workgroups sharing an
-//   M-tile's activations sit on the same L2.
+//   Scheduling: the grid's workgroups are dealt round-robin over the 8 XCDs, and each
+//   XCD's CUs take its workgroups in order.  XCD x runs M-tile ranks x, x+8, x+16, ...,
+//   each as n_ntiles consecutive workgroups (the workgroups sharing an M-tile's
+//   activations sit on one L2), where rank r is the r-th tile in an order computed on
+//   the device from token_position_to_id: most 16-slot subtiles first, all-padding
+//   tiles last.  Every XCD gets an equal share of each tile size, and the long tiles
+//   start first (a block of 256 slots holding ~130 tokens is one full tile and one
+//   nearly empty one; in M order the empty tail blocks of the mapping would all land
+//   on the last XCDs).
 // gate_up: A = x rows gathered through token_position_to_id; epilogue = bias,
 //          clamps, activation and up * act with the reference's bf16 roundings;
 //          writes h [slots, I] bf16.
@@ -49,8 +56,14 @@ struct PrefillArgs {
   uint16_t* out;          // h [slots, I] or y [slots, H]
   int T, K, N_rows, I, H, B;
   int n_mtiles, n_ntiles;
+  const int32_t* order;   // M-tile by rank (null: rank order)
   ExpertParams p;
 };
+
+// Workgroups per GEMM launch: every XCD runs the same number of M-tile ranks.
+inline unsigned prefill_grid(int n_mtiles, int n_ntiles) {
+  return (unsigned)(8 * n_ntiles * ((n_mtiles + 7) / 8));
+}
 
 __device__ __forceinline__ float rb(float v) { return round_bf16(v); }
 
@@ -330,22 +343,21 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
       sa2[kPM * 256], sa3[kPM * 256];
   __shared__ int32_t stok[kPM];
-  __shared__ int s_last;
+  __shared__ int s_last;  // last slot of the tile holding a real token, -1 if none
   auto stage = [&](auto s_c) -> uint8_t* {
     constexpr int S = decltype(s_c)::value;
     if constexpr (S == 0) return sa0;
     else if constexpr (S == 1) return sa1;
     else if constexpr (S == 2) return sa2;
     else return sa3;
-  };  // last slot of the tile holding a real token, -1 if none
+  };
 
-  // XCD-aware tile order (workgroups are dealt round-robin over the 8 XCDs).
-  const int G = args.n_mtiles * args.n_ntiles;
-  const int wg = blockIdx.x;
-  const int xcd = wg & 7, i8 = wg >> 3;
-  const int per = G >> 3, rem = G & 7;
-  const int lin = xcd * per + min(xcd, rem) + i8;
-  const int mt = lin / args.n_ntiles, nt = lin % args.n_ntiles;
+  // Workgroup -> (XCD, its i-th workgroup) -> (M-tile rank, N-tile).
+  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+  const int rank = (local / args.n_ntiles) * 8 + xcd;
+  const int nt = local % args.n_ntiles;
+  if (rank >= args.n_mtiles) return;
+  const int mt = args.order ? args.order[rank] : rank;
   const int m0 = mt * kPM;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
 
@@ -405,6 +417,72 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
 }
 
+// order[r] = the r-th M-tile by descending weight, ties in M order; the weight of a tile
+// is the number of its 16-slot subtiles whose first slot holds a real token (the GEMM's
+// subtile count when real slots come first, as the blockwise mapping lays them out;
+// a different layout only changes the schedule).  One workgroup: a histogram of the
+// weights, then a stable scatter ranked by ballots per weight.
+constexpr int kOrderThreads = 1024;
+__device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
+  int w = 0;
+#pragma unroll
+  for (int s = 0; s < kPM / 16; ++s) {
+    const int tk = tp2id[(size_t)mt * kPM + 16 * s];
+    w += (tk >= 0 && tk < T) ? 1 : 0;
+  }
+  return w;
+}
+
+__global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
+    const int32_t* __restrict__ tp2id, int n_mtiles, int T, int32_t* __restrict__ order) {
+  constexpr int NW = kPM / 16 + 1;  // weights 0..8
+  constexpr int kWaves = kOrderThreads / 64;
+  __shared__ int s_hist[NW];
+  __shared__ int s_next[NW];  // next free rank per weight
+  __shared__ int s_cnt[kWaves][NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < NW) s_hist[tid] = 0;
+  __syncthreads();
+  for (int base = 0; base < n_mtiles; base += kOrderThreads) {
+    const int mt = base + tid;
+    if (mt < n_mtiles) atomicAdd(&s_hist[tile_weight(tp2id, mt, T)], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int r = 0;
+    for (int w = NW - 1; w >= 0; --w) {
+      s_next[w] = r;
+      r += s_hist[w];
+    }
+  }
+  __syncthreads();
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < n_mtiles; base += kOrderThreads) {
+    const int mt = base + tid;
+    const int w = mt < n_mtiles ? tile_weight(tp2id, mt, T) : -1;
+    int in_wave = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const unsigned long long m = __ballot(w == v);
+      if (lane == 0) s_cnt[wave][v] = __popcll(m);
+      if (w == v) in_wave = __popcll(m & below);
+    }
+    __syncthreads();
+    if (w >= 0) {
+      int r = s_next[w] + in_wave;
+      for (int j = 0; j < wave; ++j) r += s_cnt[j][w];
+      order[r] = mt;
+    }
+    __syncthreads();
+    if (tid < NW) {
+      int c = 0;
+      for (int j = 0; j < kWaves; ++j) c += s_cnt[j][tid];
+      s_next[tid] += c;
+    }
+    __syncthreads();
+  }
+}
+
 // inv[t, e] = slot of (t, e) or -1.
 __global__ void cte_inverse_kernel(const int32_t* __restrict__ tp2id,
                                    const int32_t* __restrict__ b2e, int64_t n_slots, int B, int T,
@@ -456,6 +534,7 @@ struct CteWs {
   uint16_t* h;
   uint16_t* y;
   int32_t* inv;
+  int32_t* order;
 };
 
 static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -465,6 +544,7 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   c.h = cv.take<uint16_t>(n_slots * I);
   c.y = cv.take<uint16_t>(n_slots * H);
   c.inv = cv.take<int32_t>(T * E);
+  c.order = cv.take<int32_t>(n_slots / kPM);
   if (w) *w = c;
   return cv.off + 256;
 }
@@ -518,6 +598,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.H = (int)H;
   a.B = (int)block_size;
   a.n_mtiles = (int)(n_slots / kPM);
+  a.order = w.order;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
@@ -533,8 +614,10 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
+  hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
+                     token_position_to_id, a.n_mtiles, (int)T, w.order);
   mark(0);
-  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
                      dim3(kPThreads), 0, s, a);
   mark(1);
   // down: A = h (K = I), rows = H
@@ -546,7 +629,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)I;
   a.N_rows = (int)H;
   a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
                      dim3(kPThreads), 0, s, a);
   mark(2);
   hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
@@ -586,7 +669,7 @@ extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, con
   a.p.gate_hi = INFINITY;
   a.p.up_lo = -INFINITY;
   a.p.up_hi = INFINITY;
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)(a.n_mtiles * a.n_ntiles)),
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
                      dim3(kPThreads), 0, as_stream(stream), a);
   return check_launch("linear");
 }
