@@ -52,11 +52,10 @@ struct PrefillArgs {
   const uint8_t* ws;      // packed scales
   const uint16_t* bias;   // gate_up: [E, 2, I]; down: [E, H]; may be null
   const int32_t* tp2id;   // token_position_to_id [slots]
-  const int32_t* b2e;     // block_to_expert [n_blocks]
   uint16_t* out;          // h [slots, I] or y [slots, H]
   int T, K, N_rows, I, H, B;
   int n_mtiles, n_ntiles;
-  const int32_t* order;   // M-tile by rank (null: rank order)
+  const int2* order;      // (M-tile, its expert) by rank (null: rank order, expert 0)
   ExpertParams p;
 };
 
@@ -65,7 +64,9 @@ inline unsigned prefill_grid(int n_mtiles, int n_ntiles) {
   return (unsigned)(8 * n_ntiles * ((n_mtiles + 7) / 8));
 }
 
-__device__ __forceinline__ float rb(float v) { return round_bf16(v); }
+// Round to bf16 (nearest even) and back: the gfx950 conversion instruction, which
+// gives round_bf16's result on every non-NaN input (NaN stays NaN).
+__device__ __forceinline__ float rb(float v) { return (float)(__bf16)v; }
 
 __device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
   v = (v > hi) ? hi : v;
@@ -73,14 +74,21 @@ __device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
   return v;
 }
 
-// Activation on a bf16 value with the reference's bf16 intermediate roundings.
+// Activation on a bf16 value with the reference's bf16 intermediate roundings.  The
+// sigmoid uses the hardware exponential and reciprocal (about 1 ulp each in fp32); its
+// result is rounded to bf16 right after, so it differs from the correctly rounded
+// sigmoid only where that lies within a few fp32 ulps of a bf16 rounding boundary.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
 __device__ __forceinline__ float act_bf16(float g, int act) {
   if (act == kSwish) {
     const float t1 = rb(g * 1.702f);
-    const float t2 = rb(1.0f / (1.0f + expf(-t1)));
+    const float t2 = rb(sigmoid_fast(t1));
     return rb(g * t2);
   }
-  if (act == kSiLU) return rb(g / (1.0f + expf(-g)));
+  if (act == kSiLU) return rb(g * sigmoid_fast(g));
   return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
 }
 
@@ -286,8 +294,26 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
 
   const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  // The epilogues load their biases first, all in flight together: unconditional loads
+  // (a missing bias or a column past the tile reads element 0 of a valid array) and no
+  // store before them (the compiler cannot tell the output from the bias, and would
+  // wait for every store before a later bias load).
+  const uint16_t* bsrc = args.bias ? args.bias : reinterpret_cast<const uint16_t*>(args.wq);
   if (GATE_UP) {
     const int I = args.I;
+    float gb[2][4], ub[2][4];
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const int col0 = 16 * (rg_first / 2 + pp) + 4 * q;
+      const bool ok = args.bias && 2 * pp < p.rv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const size_t ig = ok ? (size_t)e * 2 * I + col0 + i : 0;
+        const size_t iu = ok ? (size_t)e * 2 * I + I + col0 + i : 0;
+        gb[pp][i] = bf16_bits_to_f32(bsrc[ig]);
+        ub[pp][i] = bf16_bits_to_f32(bsrc[iu]);
+      }
+    }
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       if (2 * pp >= p.rv) continue;
@@ -303,8 +329,8 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
         for (int i = 0; i < 4; ++i) {
           float g = rb(g4[i]), u = rb(u4[i]);
           if (args.bias) {
-            g = rb(g + bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + col0 + i]));
-            u = rb(u + bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + I + col0 + i]));
+            g = rb(g + gb[pp][i]);
+            u = rb(u + ub[pp][i]);
           }
           g = clamp_ref(g, args.p.gate_lo, args.p.gate_hi);
           u = clamp_ref(u, args.p.up_lo, args.p.up_hi);
@@ -316,6 +342,14 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
     }
   } else {
     const int H = args.H;
+    float bb[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n0 = 16 * (rg_first + r) + 4 * q;
+      const bool ok = args.bias && r < p.rv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bb[r][i] = bf16_bits_to_f32(bsrc[ok ? (size_t)e * H + n0 + i : 0]);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if (r >= p.rv) continue;
@@ -328,7 +362,7 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float v = rb(acc[r][t][i]);
-          if (args.bias) v = rb(v + bf16_bits_to_f32(args.bias[(size_t)e * H + n0 + i]));
+          if (args.bias) v = rb(v + bb[r][i]);
           y[i] = f32_to_bf16_bits(v);
         }
         *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * H + n0) =
@@ -343,7 +377,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
       sa2[kPM * 256], sa3[kPM * 256];
   __shared__ int32_t stok[kPM];
-  __shared__ int s_last;  // last slot of the tile holding a real token, -1 if none
+  __shared__ int s_lastw[kPM / 64];  // per wave of slots: last slot holding a real token, or -1
   auto stage = [&](auto s_c) -> uint8_t* {
     constexpr int S = decltype(s_c)::value;
     if constexpr (S == 0) return sa0;
@@ -357,25 +391,28 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   const int rank = (local / args.n_ntiles) * 8 + xcd;
   const int nt = local % args.n_ntiles;
   if (rank >= args.n_mtiles) return;
-  const int mt = args.order ? args.order[rank] : rank;
+  int mt = rank, e = 0;
+  if (args.order) {
+    const int2 me = args.order[rank];
+    mt = me.x;
+    e = me.y;
+  }
   const int m0 = mt * kPM;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
 
-  if (tid == 0) s_last = -1;
-  __syncthreads();
-  if (tid < kPM) {
+  if (tid < kPM) {  // waves 0 and 1, whole
     // Without a mapping (plain linear) slot m0 + tid is row m0 + tid of A, real below T.
     int tk = args.tp2id ? args.tp2id[m0 + tid] : (m0 + tid < args.T ? m0 + tid : -1);
     if (tk < 0 || tk >= args.T) tk = -1;
     stok[tid] = tk;
-    if (tk >= 0) atomicMax(&s_last, tid);
+    const unsigned long long real = __ballot(tk >= 0);
+    if (lane == 0) s_lastw[wave] = real ? 64 * wave + 63 - __builtin_clzll(real) : -1;
   }
   __syncthreads();
-  const int last = s_last;
+  const int last = max(s_lastw[0], s_lastw[1]);
   if (last < 0) return;
 
   PrefillTile p;
-  const int e = args.b2e ? args.b2e[m0 / args.B] : 0;
   p.K = args.K;
   p.rg_bytes = (uint32_t)p.K * 8u;
   const int n_rg_total = args.N_rows / 16;
@@ -417,11 +454,11 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
 }
 
-// order[r] = the r-th M-tile by descending weight, ties in M order; the weight of a tile
-// is the number of its 16-slot subtiles whose first slot holds a real token (the GEMM's
-// subtile count when real slots come first, as the blockwise mapping lays them out;
-// a different layout only changes the schedule).  One workgroup: a histogram of the
-// weights, then a stable scatter ranked by ballots per weight.
+// order[r] = (the r-th M-tile by descending weight, ties in M order; its expert).  The
+// weight of a tile is the number of its 16-slot subtiles whose first slot holds a real
+// token (the GEMM's subtile count when real slots come first, as the blockwise mapping
+// lays them out; a different layout only changes the schedule).  One workgroup: a
+// histogram of the weights, then a stable scatter ranked by ballots per weight.
 constexpr int kOrderThreads = 1024;
 __device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
   int w = 0;
@@ -434,7 +471,8 @@ __device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, in
 }
 
 __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
-    const int32_t* __restrict__ tp2id, int n_mtiles, int T, int32_t* __restrict__ order) {
+    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int n_mtiles,
+    int T, int2* __restrict__ order) {
   constexpr int NW = kPM / 16 + 1;  // weights 0..8
   constexpr int kWaves = kOrderThreads / 64;
   __shared__ int s_hist[NW];
@@ -471,7 +509,7 @@ __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
     if (w >= 0) {
       int r = s_next[w] + in_wave;
       for (int j = 0; j < wave; ++j) r += s_cnt[j][w];
-      order[r] = mt;
+      order[r] = int2{mt, b2e[(size_t)mt * kPM / B]};
     }
     __syncthreads();
     if (tid < NW) {
@@ -534,7 +572,7 @@ struct CteWs {
   uint16_t* h;
   uint16_t* y;
   int32_t* inv;
-  int32_t* order;
+  int2* order;
 };
 
 static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -544,7 +582,7 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   c.h = cv.take<uint16_t>(n_slots * I);
   c.y = cv.take<uint16_t>(n_slots * H);
   c.inv = cv.take<int32_t>(T * E);
-  c.order = cv.take<int32_t>(n_slots / kPM);
+  c.order = cv.take<int2>(n_slots / kPM);
   if (w) *w = c;
   return cv.off + 256;
 }
@@ -592,7 +630,6 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
 
   PrefillArgs a;
   a.tp2id = token_position_to_id;
-  a.b2e = block_to_expert;
   a.T = (int)T;
   a.I = (int)I;
   a.H = (int)H;
@@ -615,7 +652,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.N_rows = (int)(2 * I);
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
   hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
-                     token_position_to_id, a.n_mtiles, (int)T, w.order);
+                     token_position_to_id, block_to_expert, (int)block_size, a.n_mtiles, (int)T,
+                     w.order);
   mark(0);
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
                      dim3(kPThreads), 0, s, a);
