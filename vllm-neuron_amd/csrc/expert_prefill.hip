@@ -534,32 +534,66 @@ __global__ void cte_inverse_kernel(const int32_t* __restrict__ tp2id,
   inv[(size_t)tk * E + e] = (int32_t)p;
 }
 
-// out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.
-__global__ void __launch_bounds__(256) cte_combine_kernel(const uint16_t* __restrict__ y,
-                                                          const int32_t* __restrict__ inv,
-                                                          const float* __restrict__ aff, int H,
-                                                          int E, int scale_mode, int out_f32,
-                                                          void* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (n >= H) return;
-  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int e = 0; e < E; ++e) {
-    const int p = inv[(size_t)t * E + e];
-    if (p < 0) continue;
-    float a = aff[(size_t)t * E + e];
-    if (scale_mode == MXMOE_SCALE_NO) a = 1.0f;
-    const u16x4 v = *reinterpret_cast<const u16x4*>(y + (size_t)p * H + n);
+// out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.  One
+// workgroup per token: the token's (slot, weight) pairs are compacted in ascending
+// expert order from its row of inv (a ballot per 64 experts), then each thread sums
+// its 8-column groups over that list.
+constexpr int kCombineThreads = 256;
+constexpr int kCteMaxE = 1024;
+__global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
+    const float* __restrict__ aff, int H, int E, int scale_mode, int out_f32,
+    void* __restrict__ out) {
+  constexpr int kWaves = kCombineThreads / 64;
+  constexpr int kMaxChunks = kCteMaxE / 64;
+  __shared__ int s_slot[kCteMaxE];
+  __shared__ float s_w[kCteMaxE];
+  __shared__ int s_cc[kMaxChunks];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = (E + 63) / 64;
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int slot[kMaxChunks / kWaves];
+  unsigned long long m[kMaxChunks / kWaves];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
+  for (int j = 0; j < kMaxChunks / kWaves; ++j) {
+    const int e = (wave + kWaves * j) * 64 + lane;
+    slot[j] = e < E ? inv[(size_t)t * E + e] : -1;
+    m[j] = __ballot(slot[j] >= 0);
+    if (lane == 0 && wave + kWaves * j < nch) s_cc[wave + kWaves * j] = __popcll(m[j]);
   }
-  if (out_f32) {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + (size_t)t * H + n) = acc;
-  } else {
-    *reinterpret_cast<u16x4*>(static_cast<uint16_t*>(out) + (size_t)t * H + n) =
-        u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
-              f32_to_bf16_bits(acc[3])};
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kMaxChunks / kWaves; ++j) {
+    if (slot[j] < 0) continue;
+    const int ch = wave + kWaves * j, e = ch * 64 + lane;
+    int pos = __popcll(m[j] & below);
+    for (int k = 0; k < ch; ++k) pos += s_cc[k];
+    s_slot[pos] = slot[j];
+    s_w[pos] = scale_mode == MXMOE_SCALE_NO ? 1.0f : aff[(size_t)t * E + e];
+  }
+  int cnt = 0;
+  for (int k = 0; k < nch; ++k) cnt += s_cc[k];
+  __syncthreads();
+  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+  for (int n = tid * 8; n < H; n += kCombineThreads * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = 0; k < cnt; ++k) {
+      const float a = s_w[k];
+      const u16x8 v = *reinterpret_cast<const u16x8*>(y + (size_t)s_slot[k] * H + n);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
+    }
+    if (out_f32) {
+      float* o = static_cast<float*>(out) + (size_t)t * H + n;
+      *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+      *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    } else {
+      u16x8 r;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(acc[i]);
+      *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(out) + (size_t)t * H + n) = r;
+    }
   }
 }
 
@@ -609,7 +643,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   MXMOE_REQUIRE(x && affinities_masked && gu_q && gu_s && dn_q && dn_s && token_position_to_id &&
                     block_to_expert && out && workspace,
                 "moe_cte: null pointer");
-  MXMOE_REQUIRE(T >= 1 && E >= 1 && n_blocks >= 1, "moe_cte: bad T/E/n_blocks");
+  MXMOE_REQUIRE(T >= 1 && E >= 1 && E <= kCteMaxE && n_blocks >= 1,
+                "moe_cte: bad T/E/n_blocks (E at most %d)", kCteMaxE);
   MXMOE_REQUIRE(block_size >= 128 && block_size % 128 == 0,
                 "moe_cte: block_size=%lld must be a multiple of 128", (long long)block_size);
   MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
@@ -675,9 +710,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   hipLaunchKernelGGL(cte_inverse_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
                      token_position_to_id, block_to_expert, n_slots, (int)block_size, (int)T,
                      (int)E, w.inv);
-  hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
-                     dim3(256), 0, s, w.y, w.inv, affinities_masked, (int)H, (int)E, scale_mode,
-                     out_f32, out);
+  hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, s, w.y,
+                     w.inv, affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
   mark(3);
   return check_launch("moe_cte");
 }

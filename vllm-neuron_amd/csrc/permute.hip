@@ -1,76 +1,102 @@
-// Token -> expert permutation.
+// Token -> expert permutation for the prefill path (blockwise mapping), bit-exact with
+// the reference torch flow: a stable counting sort of the routed (token, expert) pairs
+// by expert, each expert's run padded with -1 to a multiple of the block size.
 //
-// (1) Blockwise mapping for the prefill path, bit-exact with the reference torch
-//     flow: a stable counting sort of routed (token, expert) pairs by expert, each
-//     expert's run padded with -1 to a multiple of the block size.
-//     Chunks of 256 tokens (4 waves x 64).  Inside a chunk every wave builds one
-//     64-bit token mask per expert in LDS (atomicOr of the lane bit); the rank of a
-//     token among the chunk's tokens of an expert is popcounts of the earlier
-//     waves' masks plus popcount(own mask & lanes below).  Per-chunk counts are
-//     scanned per expert, experts are scanned into block offsets, then tokens are
-//     scattered.  No step depends on atomic ordering, so the result is unique.
-// (2) The decode routing for moe_tkg: same ranking inside one workgroup, from
-//     top-k indices, producing per-expert slot lists and per-token slot lists.
+// Chunks of 64 tokens, one workgroup of 256 threads each: four threads per token read
+// its affinity row with 16-byte loads (each nonzero sets the token's bit in a 64-bit
+// LDS mask of its expert).  The rank of a pair among the chunk's tokens of its expert
+// is popcount(mask & tokens below); per-chunk counts are scanned per expert (one wave
+// per expert, lanes over chunks), experts are scanned into block offsets, and the pairs
+// are scattered.  No step depends on atomic ordering, so the result is unique.
 #include "capi_util.h"
 #include "common.h"
 
 namespace mxmoe {
 
-constexpr int kChunkTok = 256;
+constexpr int kChunkTok = 64;
 constexpr int kMaxE = 1024;
+constexpr int kBwThreads = 256;
 
-__device__ __forceinline__ bool routed(const float* aff_row, int e) { return aff_row[e] != 0.0f; }
+// Calls f(e, a) for the nonzero affinities of row t handled by thread quarter q
+// (four threads per row; 16-byte loads when E is a multiple of 4).
+template <typename F>
+__device__ __forceinline__ void for_row_quarter(const float* __restrict__ row, int E, int q, F f) {
+  if ((E & 3) == 0) {
+    const f32x4* r4 = reinterpret_cast<const f32x4*>(row);
+    for (int i = q; i < E / 4; i += 4) {
+      const f32x4 v = r4[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f(4 * i + j, v[j]);
+    }
+  } else {
+    for (int e = q; e < E; e += 4) f(e, row[e]);
+  }
+}
 
-// Pass 1: per-chunk expert counts and the masked affinities.
-__global__ void __launch_bounds__(256) bw_count_kernel(const float* __restrict__ aff,
-                                                       const uint8_t* __restrict__ pmask, int T,
-                                                       int E, float* __restrict__ aff_masked,
-                                                       int32_t* __restrict__ chunk_counts) {
-  extern __shared__ unsigned long long masks[];  // [4][E]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < 4 * E; i += 256) masks[i] = 0ull;
+// Pass 1: per-chunk expert masks and counts, and the masked affinities.
+// counts are stored expert-major: counts[e * n_chunks + c].
+__global__ void __launch_bounds__(kBwThreads) bw_count_kernel(
+    const float* __restrict__ aff, const uint8_t* __restrict__ pmask, int T, int E,
+    int n_chunks, float* __restrict__ aff_masked, int32_t* __restrict__ counts,
+    unsigned long long* __restrict__ chunk_masks) {
+  extern __shared__ unsigned long long masks[];  // [E]
+  const int tid = threadIdx.x, tl = tid >> 2, q = tid & 3, c = blockIdx.x;
+  for (int i = tid; i < E; i += kBwThreads) masks[i] = 0ull;
   __syncthreads();
-  const int t = blockIdx.x * kChunkTok + threadIdx.x;
+  const int t = c * kChunkTok + tl;
   if (t < T) {
     const float* row = aff + (size_t)t * E;
     float* mrow = aff_masked + (size_t)t * E;
     const float pm = pmask ? (pmask[t] ? 1.0f : 0.0f) : 1.0f;
-    for (int e = 0; e < E; ++e) {
-      const float a = row[e];
+    for_row_quarter(row, E, q, [&](int e, float a) {
       mrow[e] = pmask ? a * pm : a;
-      if (a != 0.0f) atomicOr(&masks[wave * E + e], 1ull << lane);
-    }
+      if (a != 0.0f) atomicOr(&masks[e], 1ull << tl);
+    });
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 256) {
-    int c = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) c += __popcll(masks[w * E + e]);
-    chunk_counts[(size_t)blockIdx.x * E + e] = c;
+  for (int e = tid; e < E; e += kBwThreads) {
+    const unsigned long long m = masks[e];
+    counts[(size_t)e * n_chunks + c] = __popcll(m);
+    chunk_masks[(size_t)c * E + e] = m;
   }
 }
 
-// Pass 2 (one workgroup of 1024 threads): per-expert chunk prefix, block counts,
-// block offsets, block_to_expert, conditions.
+// Pass 2 (one workgroup of 1024 threads): per-expert exclusive prefix over chunks (wave
+// per expert), block counts, block offsets, block_to_expert, conditions.
 __global__ void __launch_bounds__(1024) bw_scan_kernel(
-    int32_t* __restrict__ chunk_counts, int n_chunks, int E, int B, int N,
+    int32_t* __restrict__ counts, int n_chunks, int E, int B, int N,
     int32_t* __restrict__ expert_pos, int32_t* __restrict__ block_to_expert,
     int32_t* __restrict__ conditions, int32_t* __restrict__ expert_counts) {
-  __shared__ int cum[kMaxE];  // inclusive cumulative blocks per expert
+  __shared__ int cum[kMaxE];  // per-expert totals, then inclusive cumulative blocks
   __shared__ int wsum[16];
-  const int e = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = wave; e < E; e += 16) {
+    int32_t* ce = counts + (size_t)e * n_chunks;
+    int run = 0;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+      const int c = c0 + lane;
+      const int v = c < n_chunks ? ce[c] : 0;
+      int x = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(x, off);
+        if (lane >= off) x += o;
+      }
+      if (c < n_chunks) ce[c] = run + x - v;  // exclusive prefix within the expert
+      run += __shfl(x, 63);
+    }
+    if (lane == 0) cum[e] = run;
+  }
+  __syncthreads();
+  const int e = tid;
   int total = 0, nb = 0;
   if (e < E) {
-    for (int c = 0; c < n_chunks; ++c) {
-      const int v = chunk_counts[(size_t)c * E + e];
-      chunk_counts[(size_t)c * E + e] = total;  // exclusive prefix within the expert
-      total += v;
-    }
+    total = cum[e];
     nb = (total + B - 1) / B;
     if (expert_counts) expert_counts[e] = total;
   }
+  __syncthreads();
   // Inclusive block scan over experts: wave scan, then across waves.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int v = nb;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -88,7 +114,7 @@ __global__ void __launch_bounds__(1024) bw_scan_kernel(
   }
   __syncthreads();
   const int used = cum[E - 1];
-  for (int n = threadIdx.x; n < N; n += 1024) {
+  for (int n = tid; n < N; n += 1024) {
     // block_to_expert[n] = #{e < E-1 : n >= cum[e]}  (cum is non-decreasing)
     int lo = 0, hi = E - 1;
     while (lo < hi) {
@@ -103,29 +129,21 @@ __global__ void __launch_bounds__(1024) bw_scan_kernel(
 }
 
 // Pass 3: scatter token ids.  token_position_to_id was filled with -1 beforehand.
-__global__ void __launch_bounds__(256) bw_scatter_kernel(
-    const float* __restrict__ aff, int T, int E, const int32_t* __restrict__ chunk_prefix,
+__global__ void __launch_bounds__(kBwThreads) bw_scatter_kernel(
+    const float* __restrict__ aff, int T, int E, int n_chunks,
+    const int32_t* __restrict__ prefix, const unsigned long long* __restrict__ chunk_masks,
     const int32_t* __restrict__ expert_pos, int32_t* __restrict__ tp2id, int64_t n_slots) {
-  extern __shared__ unsigned long long masks[];  // [4][E]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < 4 * E; i += 256) masks[i] = 0ull;
-  __syncthreads();
-  const int t = blockIdx.x * kChunkTok + threadIdx.x;
-  const float* row = aff + (size_t)min(t, T - 1) * E;
-  if (t < T)
-    for (int e = 0; e < E; ++e)
-      if (routed(row, e)) atomicOr(&masks[wave * E + e], 1ull << lane);
-  __syncthreads();
+  const int tid = threadIdx.x, tl = tid >> 2, q = tid & 3, c = blockIdx.x;
+  const int t = c * kChunkTok + tl;
   if (t >= T) return;
-  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int e = 0; e < E; ++e) {
-    if (!routed(row, e)) continue;
-    int rank = chunk_prefix[(size_t)blockIdx.x * E + e];
-    for (int w = 0; w < wave; ++w) rank += __popcll(masks[w * E + e]);
-    rank += __popcll(masks[wave * E + e] & below);
+  const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
+  for_row_quarter(aff + (size_t)t * E, E, q, [&](int e, float a) {
+    if (a == 0.0f) return;
+    const int rank = prefix[(size_t)e * n_chunks + c] +
+                     __popcll(chunk_masks[(size_t)c * E + e] & below);
     const int64_t pos = (int64_t)expert_pos[e] + rank;
     if (pos < n_slots) tp2id[pos] = t;
-  }
+  });
 }
 
 __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
@@ -139,7 +157,8 @@ using namespace mxmoe;
 
 static size_t bw_ws(int64_t T, int64_t E) {
   const int64_t nch = (T + kChunkTok - 1) / kChunkTok;
-  return align_up((size_t)(nch * E) * 4, 256) + align_up((size_t)E * 4, 256) + 256;
+  return align_up((size_t)(nch * E) * 4, 256) + align_up((size_t)(nch * E) * 8, 256) +
+         align_up((size_t)E * 4, 256) + 256;
 }
 
 extern "C" size_t mxmoe_blockwise_workspace_bytes(int64_t T, int64_t E) { return bw_ws(T, E); }
@@ -169,19 +188,22 @@ extern "C" int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* p
                      bw_ws(T, E));
   Carver cv(workspace, workspace_bytes);
   const int64_t nch = (T + kChunkTok - 1) / kChunkTok;
-  int32_t* chunk_counts = cv.take<int32_t>(nch * E);
+  int32_t* counts = cv.take<int32_t>(nch * E);
+  unsigned long long* chunk_masks = cv.take<unsigned long long>(nch * E);
   int32_t* expert_pos = cv.take<int32_t>(E);
   hipStream_t s = as_stream(stream);
   const int64_t n_slots = n_blocks * block_size;
   hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
                      token_position_to_id, n_slots, -1);
-  const size_t lds = (size_t)4 * E * sizeof(unsigned long long);
-  hipLaunchKernelGGL(bw_count_kernel, dim3((unsigned)nch), dim3(256), lds, s, affinities,
-                     padding_mask, (int)T, (int)E, affinities_masked, chunk_counts);
-  hipLaunchKernelGGL(bw_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_counts, (int)nch, (int)E,
+  const size_t lds = (size_t)E * sizeof(unsigned long long);
+  hipLaunchKernelGGL(bw_count_kernel, dim3((unsigned)nch), dim3(kBwThreads), lds, s, affinities,
+                     padding_mask, (int)T, (int)E, (int)nch, affinities_masked, counts,
+                     chunk_masks);
+  hipLaunchKernelGGL(bw_scan_kernel, dim3(1), dim3(1024), 0, s, counts, (int)nch, (int)E,
                      (int)block_size, (int)n_blocks, expert_pos, block_to_expert, conditions,
                      expert_counts);
-  hipLaunchKernelGGL(bw_scatter_kernel, dim3((unsigned)nch), dim3(256), lds, s, affinities,
-                     (int)T, (int)E, chunk_counts, expert_pos, token_position_to_id, n_slots);
+  hipLaunchKernelGGL(bw_scatter_kernel, dim3((unsigned)nch), dim3(kBwThreads), 0, s, affinities,
+                     (int)T, (int)E, (int)nch, counts, chunk_masks, expert_pos,
+                     token_position_to_id, n_slots);
   return check_launch("blockwise_mapping");
 }
