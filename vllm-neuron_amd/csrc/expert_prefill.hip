@@ -17,14 +17,15 @@
 //   tiles whose 128 slots are all padding exit at once, and the waves run only the
 //   16-slot tiles up to the last one holding a real slot (rounded to 1, 2, 4 or 8).
 //   Scheduling: the grid's workgroups are dealt round-robin over the 8 XCDs, and each
-//   XCD's CUs take its workgroups in order.  XCD x runs M-tile ranks x, x+8, x+16, ...,
-//   each as n_ntiles consecutive workgroups (the workgroups sharing an M-tile's
-//   activations sit on one L2), where rank r is the r-th tile in an order computed on
-//   the device from token_position_to_id: most 16-slot subtiles first, all-padding
-//   tiles last.  Every XCD gets an equal share of each tile size, and the long tiles
-//   start first (a block of 256 slots holding ~130 tokens is one full tile and one
-//   nearly empty one; in M order the empty tail blocks of the mapping would all land
-//   on the last XCDs).
+//   XCD's CUs take its workgroups in order.  M-tiles are scheduled in groups (the tiles
+//   of one block: 2 at block size 256).  XCD x runs group ranks x, x+8, x+16, ..., each
+//   as group x n_ntiles consecutive workgroups, M-tile by M-tile (the workgroups sharing
+//   activations or weight rows sit on one L2 at about the same time), where rank r is the r-th group in an order computed on the device
+//   from token_position_to_id: most 16-slot subtiles first, all-padding groups last.
+//   Every XCD gets an equal share of each group size, and the long groups start first
+//   (a block of 256 slots holding ~130 tokens is one full tile and one nearly empty
+//   one; in M order the empty tail blocks of the mapping would all land on the last
+//   XCDs).
 // gate_up: A = x rows gathered through token_position_to_id; epilogue = bias,
 //          clamps, activation and up * act with the reference's bf16 roundings;
 //          writes h [slots, I] bf16.
@@ -55,13 +56,16 @@ struct PrefillArgs {
   uint16_t* out;          // h [slots, I] or y [slots, H]
   int T, K, N_rows, I, H, B;
   int n_mtiles, n_ntiles;
-  const int2* order;      // (M-tile, its expert) by rank (null: rank order, expert 0)
+  int group;              // M-tiles scheduled together (divides n_mtiles)
+  const int2* order;      // (first M-tile of a group, its expert) by rank (null: rank order,
+                          // expert 0)
   ExpertParams p;
 };
 
-// Workgroups per GEMM launch: every XCD runs the same number of M-tile ranks.
-inline unsigned prefill_grid(int n_mtiles, int n_ntiles) {
-  return (unsigned)(8 * n_ntiles * ((n_mtiles + 7) / 8));
+// Workgroups per GEMM launch: every XCD runs the same number of group ranks.
+inline unsigned prefill_grid(int n_mtiles, int n_ntiles, int group) {
+  const int n_groups = n_mtiles / group;
+  return (unsigned)(8 * group * n_ntiles * ((n_groups + 7) / 8));
 }
 
 // Round to bf16 (nearest even) and back: the gfx950 conversion instruction, which
@@ -386,15 +390,19 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     else return sa3;
   };
 
-  // Workgroup -> (XCD, its i-th workgroup) -> (M-tile rank, N-tile).
+  // Workgroup -> (XCD, its i-th workgroup) -> (group rank, M-tile in the group, N-tile).
+  // Consecutive workgroups of an XCD go to its shader engines in turn, so each M-tile of
+  // a group takes its N-tiles in a row (alternating M-tiles would send the full tiles to
+  // half of the engines).
+  const int G = args.group, per_group = G * args.n_ntiles;
   const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
-  const int rank = (local / args.n_ntiles) * 8 + xcd;
-  const int nt = local % args.n_ntiles;
-  if (rank >= args.n_mtiles) return;
-  int mt = rank, e = 0;
+  const int rank = (local / per_group) * 8 + xcd;
+  const int sub = (local % per_group) / args.n_ntiles, nt = local % args.n_ntiles;
+  if (rank >= args.n_mtiles / G) return;
+  int mt = rank * G + sub, e = 0;
   if (args.order) {
     const int2 me = args.order[rank];
-    mt = me.x;
+    mt = me.x + sub;
     e = me.y;
   }
   const int m0 = mt * kPM;
@@ -454,71 +462,96 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
     prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
 }
 
-// order[r] = (the r-th M-tile by descending weight, ties in M order; its expert).  The
-// weight of a tile is the number of its 16-slot subtiles whose first slot holds a real
-// token (the GEMM's subtile count when real slots come first, as the blockwise mapping
-// lays them out; a different layout only changes the schedule).  One workgroup: a
-// histogram of the weights, then a stable scatter ranked by ballots per weight.
+// The gate_up GEMM schedules M-tiles in groups of G consecutive tiles of one block (G =
+// the largest power of two up to 16 dividing B / 128): the group's workgroups run one
+// after another on one XCD, so a block's second, mostly empty M-tile reads the weight
+// rows while the first one's workgroups hold them in L2.
+constexpr int kMaxGroupTiles = 16;
+inline int prefill_group_tiles(int64_t block_size) {
+  const int64_t per = block_size / kPM;
+  int g = 1;
+  while (g < kMaxGroupTiles && per % (2 * g) == 0) g *= 2;
+  return g;
+}
+
+// order[r] = (first M-tile of the r-th group by descending weight, ties in M order; the
+// group's expert).  The weight of a tile is the number of its 16-slot subtiles whose
+// first slot holds a real token (the GEMM's subtile count when real slots come first,
+// as the blockwise mapping lays them out; a different layout only changes the
+// schedule), a group's the sum over its tiles.  One workgroup: a histogram of the
+// weights, then a stable scatter ranked by ballots per weight.
 constexpr int kOrderThreads = 1024;
-__device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
+constexpr int kMaxWeights = kMaxGroupTiles * (kPM / 16) + 1;
+__device__ __forceinline__ int group_weight(const int32_t* __restrict__ tp2id, int g, int G,
+                                            int T) {
   int w = 0;
-#pragma unroll
-  for (int s = 0; s < kPM / 16; ++s) {
-    const int tk = tp2id[(size_t)mt * kPM + 16 * s];
+  for (int s = 0; s < G * (kPM / 16); ++s) {
+    const int tk = tp2id[(size_t)g * G * kPM + 16 * s];
     w += (tk >= 0 && tk < T) ? 1 : 0;
   }
   return w;
 }
 
-__global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
-    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int n_mtiles,
-    int T, int2* __restrict__ order) {
-  constexpr int NW = kPM / 16 + 1;  // weights 0..8
-  constexpr int kWaves = kOrderThreads / 64;
-  __shared__ int s_hist[NW];
-  __shared__ int s_next[NW];  // next free rank per weight
-  __shared__ int s_cnt[kWaves][NW];
+constexpr int kOrderWaves = kOrderThreads / 64;
+struct OrderLds {
+  int hist[kMaxWeights];
+  int next[kMaxWeights];  // next free rank per weight
+  int cnt[kOrderWaves][kMaxWeights];
+};
+
+__device__ void order_pass(const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e,
+                           int B, int n_groups, int G, int T, int2* __restrict__ order,
+                           OrderLds& L) {
+  const int NW = G * (kPM / 16) + 1;  // weights 0 .. 8G
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < NW) s_hist[tid] = 0;
+  for (int v = tid; v < NW; v += kOrderThreads) L.hist[v] = 0;
   __syncthreads();
-  for (int base = 0; base < n_mtiles; base += kOrderThreads) {
-    const int mt = base + tid;
-    if (mt < n_mtiles) atomicAdd(&s_hist[tile_weight(tp2id, mt, T)], 1);
+  for (int base = 0; base < n_groups; base += kOrderThreads) {
+    const int g = base + tid;
+    if (g < n_groups) atomicAdd(&L.hist[group_weight(tp2id, g, G, T)], 1);
   }
   __syncthreads();
   if (tid == 0) {
     int r = 0;
     for (int w = NW - 1; w >= 0; --w) {
-      s_next[w] = r;
-      r += s_hist[w];
+      L.next[w] = r;
+      r += L.hist[w];
     }
   }
   __syncthreads();
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < n_mtiles; base += kOrderThreads) {
-    const int mt = base + tid;
-    const int w = mt < n_mtiles ? tile_weight(tp2id, mt, T) : -1;
+  for (int base = 0; base < n_groups; base += kOrderThreads) {
+    const int g = base + tid;
+    const int w = g < n_groups ? group_weight(tp2id, g, G, T) : -1;
     int in_wave = 0;
-#pragma unroll
     for (int v = 0; v < NW; ++v) {
       const unsigned long long m = __ballot(w == v);
-      if (lane == 0) s_cnt[wave][v] = __popcll(m);
+      if (lane == 0) L.cnt[wave][v] = __popcll(m);
       if (w == v) in_wave = __popcll(m & below);
     }
     __syncthreads();
     if (w >= 0) {
-      int r = s_next[w] + in_wave;
-      for (int j = 0; j < wave; ++j) r += s_cnt[j][w];
-      order[r] = int2{mt, b2e[(size_t)mt * kPM / B]};
+      int r = L.next[w] + in_wave;
+      for (int j = 0; j < wave; ++j) r += L.cnt[j][w];
+      order[r] = int2{g * G, b2e[(size_t)g * G * kPM / B]};
     }
     __syncthreads();
-    if (tid < NW) {
+    for (int v = tid; v < NW; v += kOrderThreads) {
       int c = 0;
-      for (int j = 0; j < kWaves; ++j) c += s_cnt[j][tid];
-      s_next[tid] += c;
+      for (int j = 0; j < kOrderWaves; ++j) c += L.cnt[j][v];
+      L.next[v] += c;
     }
     __syncthreads();
   }
+}
+
+// Two orders: groups of G M-tiles for the gate_up GEMM, single M-tiles for the down GEMM.
+__global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
+    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int n_mtiles,
+    int G, int T, int2* __restrict__ order_gu, int2* __restrict__ order_dn) {
+  __shared__ OrderLds L;
+  order_pass(tp2id, b2e, B, n_mtiles / G, G, T, order_gu, L);
+  order_pass(tp2id, b2e, B, n_mtiles, 1, T, order_dn, L);
 }
 
 // inv[t, e] = slot of (t, e) or -1.
@@ -606,7 +639,8 @@ struct CteWs {
   uint16_t* h;
   uint16_t* y;
   int32_t* inv;
-  int2* order;
+  int2* order_gu;
+  int2* order_dn;
 };
 
 static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -616,7 +650,8 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   c.h = cv.take<uint16_t>(n_slots * I);
   c.y = cv.take<uint16_t>(n_slots * H);
   c.inv = cv.take<int32_t>(T * E);
-  c.order = cv.take<int2>(n_slots / kPM);
+  c.order_gu = cv.take<int2>(n_slots / kPM);
+  c.order_dn = cv.take<int2>(n_slots / kPM);
   if (w) *w = c;
   return cv.off + 256;
 }
@@ -670,7 +705,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.H = (int)H;
   a.B = (int)block_size;
   a.n_mtiles = (int)(n_slots / kPM);
-  a.order = w.order;
+  a.group = prefill_group_tiles(block_size);
+  a.order = w.order_gu;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
@@ -687,10 +723,10 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.N_rows = (int)(2 * I);
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
   hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
-                     token_position_to_id, block_to_expert, (int)block_size, a.n_mtiles, (int)T,
-                     w.order);
+                     token_position_to_id, block_to_expert, (int)block_size, a.n_mtiles, a.group,
+                     (int)T, w.order_gu, w.order_dn);
   mark(0);
-  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
+  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);
   mark(1);
   // down: A = h (K = I), rows = H
@@ -702,7 +738,11 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)I;
   a.N_rows = (int)H;
   a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
+  // Single M-tiles: at H = 2880 a tile has 6 N-tiles, and a group's run of full-tile
+  // workgroups then lands unevenly on an XCD's 4 shader engines (measured slower).
+  a.group = 1;
+  a.order = w.order_dn;
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);
   mark(2);
   hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
@@ -737,11 +777,12 @@ extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, con
   a.B = kPM;
   a.n_mtiles = (int)((M + kPM - 1) / kPM);
   a.n_ntiles = (int)((N / 16 + kPRG - 1) / kPRG);
+  a.group = 1;
   a.p.gate_lo = -INFINITY;
   a.p.gate_hi = INFINITY;
   a.p.up_lo = -INFINITY;
   a.p.up_hi = INFINITY;
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles)),
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, as_stream(stream), a);
   return check_launch("linear");
 }
