@@ -176,7 +176,7 @@ int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_
  * for an already-normalized input; semantics of moe_block_tkg.py:152-297.
  * router_w bf16 [E, H], router_b bf16 [E] or NULL; logits_out fp32 [T, E] or NULL.
  * stage_events: NULL, or 6 hipEvent_t recorded before the router and after the router,
- * routing, gate_up, down and combine kernels.  For T <= 128 one kernel takes the top-k
+ * routing, gate_up, down and combine kernels.  For T <= 16 one kernel takes the top-k
  * and routes the batch: the events after the router and after routing then both follow
  * it (routing shows no time of its own).
  */

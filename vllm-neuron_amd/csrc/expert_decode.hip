@@ -2,7 +2,8 @@
 // experts the batch selected, fp32 arithmetic as in the reference decode flow.
 //
 //   front end  (mxmoe_moe_decode, T <= 128) router logits split over many workgroups,
-//              then one workgroup for the top-k of every token and the routing below
+//              then the top-k of every token (one workgroup per 16 tokens) and the
+//              routing below; up to 16 tokens, one workgroup takes both
 //   route      one workgroup: per-expert slot lists (tokens ascending inside an
 //              expert), the list of active experts, per-token slots sorted by expert
 //   gate_up    streaming kernel, one wave per item (active expert, 4 row groups =
@@ -137,8 +138,9 @@ __global__ void __launch_bounds__(1024) tkg_route_kernel(
 
 // Decode front end for small batches: router logits as 16-token x 16-expert MFMA tiles
 // whose K reduction is split over kFrontSlices workgroups (so the router weights stream
-// through many CUs), then one workgroup that adds the partial sums, takes the top-k of
-// every token and routes the batch.
+// through many CUs), then the partial sums added, the top-k of every token and the
+// routing: one workgroup for all three up to 16 tokens, else a top-k workgroup per 16
+// tokens and the routing kernel.
 constexpr int kFrontMaxT = 128;  // larger batches take the standalone router kernels
 constexpr int kFrontSlices = 4;
 constexpr int kFrontWaves = 16 / kFrontSlices;  // waves per workgroup
@@ -242,6 +244,55 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
   __syncthreads();
   tkg_route_block(s_idx, s_val, T, K, E, scale_mode, expert_off, active, n_active, slot_tok,
                   tok_slot, tok_w);
+}
+
+// The top-k of 16 tokens per workgroup of 256 threads (token t by the 16-lane row t % 16,
+// as in front_route_kernel), the selections stored for the routing kernel: the top-k
+// work, the front end's VALU-bound part, then spreads over T / 16 CUs.
+template <int PER>
+__global__ void __launch_bounds__(256) front_topk_kernel(
+    const float* __restrict__ part, const uint16_t* __restrict__ bias, float* __restrict__ logits,
+    int T, int E, int K, int act, int act_first, int renorm, float renorm_eps,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
+  const int tid = threadIdx.x, j = tid & 15;
+  const int t = blockIdx.x * 16 + (tid >> 4);
+  if (t >= T) return;  // whole 16-lane rows
+  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(part);
+  uint16_t braw[PER];
+  float pv[kFrontSlices][PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) braw[i] = bsrc[min(j + 16 * i, E - 1)];
+#pragma unroll
+  for (int sl = 0; sl < kFrontSlices; ++sl)
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      pv[sl][i] = part[((size_t)sl * T + t) * E + min(j + 16 * i, E - 1)];
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    float a = pv[0][i];
+#pragma unroll
+    for (int sl = 1; sl < kFrontSlices; ++sl) a += pv[sl][i];
+    a += bias ? bf16_bits_to_f32(braw[i]) : 0.f;
+    const int e = j + 16 * i;
+    if (e < E) logits[(size_t)t * E + e] = a;
+    v[i] = e < E ? a : -INFINITY;
+  }
+  int sel_idx[8];
+  float out[8];
+  topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+  if (j < K) {
+    int si = 0;
+    float so = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k == j) {
+        si = sel_idx[k];
+        so = out[k];
+      }
+    topk_idx[(size_t)t * K + j] = si;
+    topk_val[(size_t)t * K + j] = so;
+  }
 }
 
 // Experts per lane of a 16-lane row: the template argument of front_route_kernel.
@@ -745,10 +796,19 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
                        dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16), kFrontSlices),
                        dim3(64 * kFrontWaves), 0, s, x, router_w, d.part, (int)T, (int)H, (int)E);
     const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
+    // One token tile: one workgroup takes the top-k and routes (one launch less).  More
+    // tiles: the top-k spreads over a workgroup per tile, then the routing kernel.
+    const bool fused = T <= 16;
 #define MXMOE_FRONT(P)                                                                       \
-  hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b, logits, \
-                     (int)T, (int)E, top_k, router_act, af, rn, renorm_eps, scale_mode,        \
-                     w.expert_off, w.active, w.n_active, w.slot_tok, w.tok_slot, w.tok_w)
+  if (fused)                                                                                 \
+    hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b,    \
+                       logits, (int)T, (int)E, top_k, router_act, af, rn, renorm_eps,         \
+                       scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok, w.tok_slot, \
+                       w.tok_w);                                                              \
+  else                                                                                       \
+    hipLaunchKernelGGL(front_topk_kernel<P>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, s, \
+                       d.part, router_b, logits, (int)T, (int)E, top_k, router_act, af, rn,    \
+                       renorm_eps, d.idx, d.val)
     switch (front_per_lane((int)E)) {
       case 1: MXMOE_FRONT(1); break;
       case 2: MXMOE_FRONT(2); break;
@@ -760,9 +820,9 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
 #undef MXMOE_FRONT
     rc = check_launch("moe_decode front end");
     if (rc) return rc;
-    return tkg_pipeline(x, nullptr, nullptr, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I,
-                        E, top_k, act, clamps, scale_mode, out, w,
-                        stage_events ? stage_events + 1 : nullptr, s, /*routed=*/true);
+    return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
+                        top_k, act, clamps, scale_mode, out, w,
+                        stage_events ? stage_events + 1 : nullptr, s, /*routed=*/fused);
   }
   rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
                   renorm_eps, logits, nullptr, d.idx, d.val, s);
