@@ -42,9 +42,12 @@
 namespace mxmoe {
 
 constexpr int kPM = 128;      // slots per M-tile
-constexpr int kPRG = 32;      // row groups per N-tile (512 rows), 4 per wave
+constexpr int kPRG = 32;      // row groups per N-tile (512 rows)
 constexpr int kPWaves = 8;
 constexpr int kPThreads = 64 * kPWaves;
+constexpr int kPRGW = kPRG / kPWaves;         // row groups per wave (whole scale quads)
+constexpr int kPDma = kPM / kPWaves / 4;      // direct loads (1 KiB = 4 rows) per wave and chunk
+static_assert(kPRGW == 4 || kPRGW == 8, "a wave holds one or two quads of row groups");
 constexpr int kPStages = 4;   // activation chunks in LDS
 
 struct PrefillArgs {
@@ -99,7 +102,7 @@ __device__ __forceinline__ float act_bf16(float g, int act) {
 // Per-workgroup and per-wave constants of a tile.
 struct PrefillTile {
   const char* a;             // activations
-  uint32_t a_off[4];         // byte offsets of this lane's four source rows (padding: a real row)
+  uint32_t a_off[kPDma];     // byte offsets of this lane's source rows (padding: a real row)
   const uint8_t* wq;         // this wave's first row group
   const uint8_t* ws;         // this wave's scale quad
   uint32_t rg_bytes;
@@ -107,11 +110,11 @@ struct PrefillTile {
   int K, nc, nfull, tail_q;
 };
 
-// One weight chunk of a wave in registers: 4 row groups x 16 B per lane, and the
-// 32-bit scale word of its quad.
+// One weight chunk of a wave in registers: kPRGW row groups x 16 B per lane, and the
+// 32-bit scale word of each quad of row groups.
 struct PrefillB {
-  u32x4 w[4];
-  uint32_t s;
+  u32x4 w[kPRGW];
+  uint32_t s[kPRGW / 4];
 };
 
 // The activation stages are separate arrays of the kernel, chosen at compile time by a
@@ -122,8 +125,9 @@ struct PrefillB {
 template <int S>
 using StageC = std::integral_constant<int, S>;
 
-// Direct loads of chunk c's activations into LDS: wave w brings rows 16w .. 16w + 15,
-// 4 x 1 KiB (rows 16w + 4i + lane / 16).  The lane's LDS slot (lane % 16) of row r holds
+// Direct loads of chunk c's activations into LDS: wave w brings its kPM / kPWaves rows,
+// kPDma x 1 KiB (rows (kPM / kPWaves) w + 4i + lane / 16).  The lane's LDS slot
+// (lane % 16) of row r holds
 // column block (lane % 16) ^ (r % 16); columns past K read column 0 of the row.  Issued
 // from inline assembly (M0 = the 1 KiB's LDS address, 16 B per lane): the compiler then
 // keeps no account of them, which it could only settle, across the loop, with a full
@@ -131,12 +135,12 @@ using StageC = std::integral_constant<int, S>;
 __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kPDma; ++i) {
     const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
     const int kcol = c * 128 + swz * 8;
     const uint32_t off = p.a_off[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
     const char* src = p.a + off;
-    uint8_t* dst = sa + (16 * wave + 4 * i) * 256;
+    uint8_t* dst = sa + ((kPM / kPWaves) * wave + 4 * i) * 256;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
@@ -145,7 +149,8 @@ __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, i
 }
 
 // The wave's weights and scales of chunk c (lanes past K re-read lane 0's bytes of the
-// chunk, row groups past the tile re-read its last valid one), 5 loads.  They are issued
+// chunk, row groups past the tile re-read its last valid one, a quad past the tile the
+// first quad's scales), kPRGW + kPRGW / 4 loads.  They are issued
 // from inline assembly, so the compiler does not track them: with direct-to-LDS loads
 // in flight as well it cannot count the wait for register loads and would drain every
 // load (s_waitcnt vmcnt(0)) before their first use.  The compiler takes the outputs as
@@ -158,13 +163,17 @@ __device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p
   const bool ok = (c < p.nfull) || ((lane >> 4) < p.tail_q);
   const uint32_t lo = ok ? (uint32_t)lane : 0u;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < kPRGW; ++r) {
     const uint32_t rr = r < p.rv ? r : p.rv - 1;
     const uint8_t* src = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u + lo * 16u;
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(f.w[r]) : "v"(src) : "memory");
   }
-  const uint8_t* ssrc = p.ws + (uint32_t)c * 256u + lo * 4u;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(f.s) : "v"(ssrc) : "memory");
+#pragma unroll
+  for (int h = 0; h < kPRGW / 4; ++h) {
+    const uint32_t qq = 4 * h < p.rv ? h : 0;
+    const uint8_t* ssrc = p.ws + qq * (uint32_t)(2 * p.K) + (uint32_t)c * 256u + lo * 4u;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(f.s[h]) : "v"(ssrc) : "memory");
+  }
 }
 
 // Waits until at most N vector memory operations issued after slot f's loads are
@@ -173,10 +182,18 @@ __device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p
 template <int N>
 __device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%5)"
-               : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.s)
-               : "n"(N)
-               : "memory");
+  if constexpr (kPRGW == 4) {
+    asm volatile("s_waitcnt vmcnt(%5)"
+                 : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.s[0])
+                 : "n"(N)
+                 : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(%10)"
+                 : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.w[4]),
+                   "+v"(f.w[5]), "+v"(f.w[6]), "+v"(f.w[7]), "+v"(f.s[0]), "+v"(f.s[1])
+                 : "n"(N)
+                 : "memory");
+  }
 }
 
 // acc[r][t] += W[row group r] x A[16-slot tile t] over chunk c.  Lanes past K get a zero
@@ -184,26 +201,27 @@ __device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
 template <int NT>
 __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const PrefillB& f,
                                                 const PrefillTile& p, int c,
-                                                f32x4 (&acc)[4][NT]) {
+                                                f32x4 (&acc)[kPRGW][NT]) {
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const bool kok = (c < p.nfull) || (q < p.tail_q);
-  float sc[4];
+  float sc[kPRGW];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) sc[r] = kok ? e8m0_to_f32((f.s >> (8 * r)) & 0xffu) : 0.0f;
-  // Per 32-wide step: the four row groups' weights dequantized once, then one
-  // activation fragment at a time against them (few registers live).
+  for (int r = 0; r < kPRGW; ++r)
+    sc[r] = kok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
+  // Per 32-wide step: the row groups' weights dequantized once, then one activation
+  // fragment at a time against them (few registers live).
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int blk = (4 * q + j) ^ (lane & 15);
-    bf16x8 wf[4];
+    bf16x8 wf[kPRGW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
+    for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const u32x4 xv =
           *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
+      for (int r = 0; r < kPRGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
     }
   }
 }
@@ -217,23 +235,28 @@ __device__ __forceinline__ void prefill_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// One chunk: chunk c is in stage S.  Issue order (the vmcnt arithmetic depends on it):
-// prologue: weights of chunks 0 and 1 (2 x 5), direct loads of chunks 0, 1, 2 (3 x 4);
-// step c: [barrier] direct loads of chunk c + 3 (4), [wait] the MFMAs of chunk c, the
-// weights of chunk c + 2 (5).
-//  - barrier: chunk c's direct loads have landed once at most 8 later loads are
-//    outstanding at step 0 and 13 at later steps (exactly 13 at step 1, more later:
-//    the wait then also covers loads two or more steps old);
-//  - weights of chunk c: at most 13 later loads outstanding (exactly 13 from step 2 on;
-//    steps 0 and 1 wait a little longer, once).
+// One chunk: chunk c is in stage S.  Issue order (the vmcnt arithmetic depends on it),
+// with D = kPDma direct loads and L = kPRGW + kPRGW / 4 weight and scale loads per chunk:
+// prologue: weights of chunks 0 and 1 (2 x L), direct loads of chunks 0, 1, 2 (3 x D);
+// step c: [barrier] direct loads of chunk c + 3 (D), [wait] the MFMAs of chunk c, the
+// weights of chunk c + 2 (L).
+//  - barrier: chunk c's direct loads have landed once at most 2D later loads are
+//    outstanding at step 0 and 2D + L at later steps (exactly that at step 1, more
+//    later: the wait then also covers loads two or more steps old); a wave without
+//    weights issues direct loads only: 2D at every step;
+//  - weights of chunk c: at most 2D + L later loads outstanding (exactly that from step
+//    2 on; steps 0 and 1 wait a little longer, once).
+constexpr int kPWaitFirst = 2 * kPDma;
+constexpr int kPWait = 2 * kPDma + kPRGW + kPRGW / 4;
 template <int S, int NT, bool ACTIVE, bool FIRST, typename Stage>
 __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
-                                             const PrefillTile& p, int c, f32x4 (&acc)[4][NT]) {
-  prefill_barrier<(FIRST || !ACTIVE) ? 8 : 13>();
+                                             const PrefillTile& p, int c,
+                                             f32x4 (&acc)[kPRGW][NT]) {
+  prefill_barrier<(FIRST || !ACTIVE) ? kPWaitFirst : kPWait>();
   prefill_dma(stage(StageC<(S + 3) % kPStages>()), p, min(c + 3, p.nc - 1));
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
-    prefill_wait_b<13>(f[S % 2]);
+    prefill_wait_b<kPWait>(f[S % 2]);
     prefill_compute<NT>(stage(StageC<S>()), f[S % 2], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
     prefill_load_b(f[S % 2], p, min(c + 2, p.nc - 1));
@@ -243,7 +266,7 @@ __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2
 
 template <int NT, bool ACTIVE, typename Stage>
 __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTile& p,
-                                             f32x4 (&acc)[4][NT]) {
+                                             f32x4 (&acc)[kPRGW][NT]) {
   PrefillB f[2];
   if constexpr (ACTIVE) {
     prefill_load_b(f[0], p, 0);
@@ -274,12 +297,8 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
   // the ring's registers are operands here, so the compiler keeps them allocated until
   // their last (unused) loads have written them.
   if constexpr (ACTIVE) {
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(f[0].w[0]), "+v"(f[0].w[1]), "+v"(f[0].w[2]), "+v"(f[0].w[3]),
-                   "+v"(f[0].s), "+v"(f[1].w[0]), "+v"(f[1].w[1]), "+v"(f[1].w[2]),
-                   "+v"(f[1].w[3]), "+v"(f[1].s)
-                 :
-                 : "memory");
+    prefill_wait_b<0>(f[0]);
+    prefill_wait_b<0>(f[1]);
   } else {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -289,9 +308,9 @@ template <bool GATE_UP, int NT, typename Stage>
 __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArgs& args,
                                             const PrefillTile& p, const int32_t* stok, int m0,
                                             int e, int rg_first) {
-  f32x4 acc[4][NT];
+  f32x4 acc[kPRGW][NT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < kPRGW; ++r)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   prefill_loop<NT, true>(stage, p, acc);
@@ -305,9 +324,9 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
   const uint16_t* bsrc = args.bias ? args.bias : reinterpret_cast<const uint16_t*>(args.wq);
   if (GATE_UP) {
     const int I = args.I;
-    float gb[2][4], ub[2][4];
+    float gb[kPRGW / 2][4], ub[kPRGW / 2][4];
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
+    for (int pp = 0; pp < kPRGW / 2; ++pp) {
       const int col0 = 16 * (rg_first / 2 + pp) + 4 * q;
       const bool ok = args.bias && 2 * pp < p.rv;
 #pragma unroll
@@ -319,7 +338,7 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
       }
     }
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
+    for (int pp = 0; pp < kPRGW / 2; ++pp) {
       if (2 * pp >= p.rv) continue;
       const int P = rg_first / 2 + pp;  // pair index = 16 intermediate columns
       const int col0 = 16 * P + 4 * q;
@@ -346,16 +365,16 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
     }
   } else {
     const int H = args.H;
-    float bb[4][4];
+    float bb[kPRGW][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kPRGW; ++r) {
       const int n0 = 16 * (rg_first + r) + 4 * q;
       const bool ok = args.bias && r < p.rv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) bb[r][i] = bf16_bits_to_f32(bsrc[ok ? (size_t)e * H + n0 + i : 0]);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kPRGW; ++r) {
       if (r >= p.rv) continue;
       const int n0 = 16 * (rg_first + r) + 4 * q;
 #pragma unroll
@@ -377,7 +396,9 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
 }
 
 template <bool GATE_UP>
-__global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs args) {
+__global__ void __launch_bounds__(kPThreads)
+    __attribute__((amdgpu_waves_per_eu(kPWaves / 4, kPWaves / 4))) prefill_gemm_kernel(
+        PrefillArgs args) {
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
       sa2[kPM * 256], sa3[kPM * 256];
   __shared__ int32_t stok[kPM];
@@ -426,8 +447,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   const int n_rg_total = args.N_rows / 16;
   const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds whole scale quads
   const int rg_valid = min(kPRG, n_rg_total - rg0);
-  const int rg_first = rg0 + 4 * wave;
-  p.rv = min(4, rg_valid - 4 * wave);
+  const int rg_first = rg0 + kPRGW * wave;
+  p.rv = min(kPRGW, rg_valid - kPRGW * wave);
   const int rgw = p.rv > 0 ? rg_first : rg0;  // waves without rows point at valid data
   p.wq = args.wq + ((size_t)e * n_rg_total + rgw) * p.rg_bytes;
   p.ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rgw / 4) * (size_t)(2 * p.K);
@@ -436,8 +457,8 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   p.tail_q = (p.K % 128) / 32;
   p.a = reinterpret_cast<const char*>(args.a);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 4 * i + (lane >> 4);
+  for (int i = 0; i < kPDma; ++i) {
+    const int row = (kPM / kPWaves) * wave + 4 * i + (lane >> 4);
     const int tk = stok[row];
     // Padding slots read a real row (token 0 / the tile's first slot): an MFMA output
     // column depends on its own slot only, and padding columns are never stored.
@@ -447,7 +468,7 @@ __global__ void __launch_bounds__(kPThreads) prefill_gemm_kernel(PrefillArgs arg
   if (p.rv <= 0) {
     // No row groups in this tile for this wave: it still brings its share of the
     // activations and meets the barriers.
-    f32x4 none[4][1];
+    f32x4 none[kPRGW][1];
     prefill_loop<1, false>(stage, p, none);
     return;
   }
