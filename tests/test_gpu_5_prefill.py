@@ -106,3 +106,35 @@ def test_prefill_and_decode_partial_chunks(dev):
     got = layer.decode(x.to(dev)).cpu()
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode small K")
+
+
+@pytest.mark.parametrize("block", [128, 384, 512, 1024])
+def test_moe_cte_block_sizes(dev, block):
+    """moe_cte at block sizes whose M-tiles the gate_up GEMM schedules in groups of 1,
+    1, 4 and 8 (block / 128 tiles, the largest power of two dividing it, at most 16)."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 37, dev, exp=(118, 122))
+    T = 300
+    x = synthetic.tokens(37, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), 8, 2, block)
+    w = layer.w
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, b2e, block, conditions=cond,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function="Swish", skip_token=True,
+                     expert_affinities_scaling_mode="POST_SCALE",
+                     gate_clamp_upper_limit=7.0, up_clamp_upper_limit=7.0,
+                     up_clamp_lower_limit=-7.0).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, 8, 2, block)
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, am_r, gu, ref.down, gb, db, gate_clamp_upper_limit=7.0,
+                             up_clamp_upper_limit=7.0, up_clamp_lower_limit=-7.0,
+                             activation_function="Swish")
+    check_close(got, want, ties, f"moe_cte block {block}")
