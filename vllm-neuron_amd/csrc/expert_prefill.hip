@@ -503,11 +503,12 @@ inline int prefill_group_tiles(int64_t block_size) {
 // weights, then a stable scatter ranked by ballots per weight.
 constexpr int kOrderThreads = 1024;
 constexpr int kMaxWeights = kMaxGroupTiles * (kPM / 16) + 1;
-__device__ __forceinline__ int group_weight(const int32_t* __restrict__ tp2id, int g, int G,
-                                            int T) {
+constexpr int kOrderMaxTiles = 10240;  // 5 B of LDS per M-tile (with the sort tables < 64 KiB)
+__device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
   int w = 0;
-  for (int s = 0; s < G * (kPM / 16); ++s) {
-    const int tk = tp2id[(size_t)g * G * kPM + 16 * s];
+#pragma unroll
+  for (int s = 0; s < kPM / 16; ++s) {
+    const int tk = tp2id[(size_t)mt * kPM + 16 * s];
     w += (tk >= 0 && tk < T) ? 1 : 0;
   }
   return w;
@@ -520,16 +521,21 @@ struct OrderLds {
   int cnt[kOrderWaves][kMaxWeights];
 };
 
-__device__ void order_pass(const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e,
-                           int B, int n_groups, int G, int T, int2* __restrict__ order,
-                           OrderLds& L) {
+// One sort over the tile weights and experts staged in LDS (s_w, s_e).
+__device__ void order_pass(const uint8_t* s_w, const int32_t* s_e, int n_groups, int G,
+                           int2* __restrict__ order, OrderLds& L) {
   const int NW = G * (kPM / 16) + 1;  // weights 0 .. 8G
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto weight = [&](int g) {
+    int w = 0;
+    for (int i = 0; i < G; ++i) w += s_w[g * G + i];
+    return w;
+  };
   for (int v = tid; v < NW; v += kOrderThreads) L.hist[v] = 0;
   __syncthreads();
   for (int base = 0; base < n_groups; base += kOrderThreads) {
     const int g = base + tid;
-    if (g < n_groups) atomicAdd(&L.hist[group_weight(tp2id, g, G, T)], 1);
+    if (g < n_groups) atomicAdd(&L.hist[weight(g)], 1);
   }
   __syncthreads();
   if (tid == 0) {
@@ -543,7 +549,7 @@ __device__ void order_pass(const int32_t* __restrict__ tp2id, const int32_t* __r
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int base = 0; base < n_groups; base += kOrderThreads) {
     const int g = base + tid;
-    const int w = g < n_groups ? group_weight(tp2id, g, G, T) : -1;
+    const int w = g < n_groups ? weight(g) : -1;
     int in_wave = 0;
     for (int v = 0; v < NW; ++v) {
       const unsigned long long m = __ballot(w == v);
@@ -554,7 +560,7 @@ __device__ void order_pass(const int32_t* __restrict__ tp2id, const int32_t* __r
     if (w >= 0) {
       int r = L.next[w] + in_wave;
       for (int j = 0; j < wave; ++j) r += L.cnt[j][w];
-      order[r] = int2{g * G, b2e[(size_t)g * G * kPM / B]};
+      order[r] = int2{g * G, s_e[g * G]};
     }
     __syncthreads();
     for (int v = tid; v < NW; v += kOrderThreads) {
@@ -567,12 +573,21 @@ __device__ void order_pass(const int32_t* __restrict__ tp2id, const int32_t* __r
 }
 
 // Two orders: groups of G M-tiles for the gate_up GEMM, single M-tiles for the down GEMM.
+// The tiles' weights and experts are read once into LDS (dynamic: 5 B per tile).
 __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
     const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int n_mtiles,
     int G, int T, int2* __restrict__ order_gu, int2* __restrict__ order_dn) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
+  int32_t* s_e = reinterpret_cast<int32_t*>(order_dyn);
+  uint8_t* s_w = order_dyn + 4 * (size_t)n_mtiles;
   __shared__ OrderLds L;
-  order_pass(tp2id, b2e, B, n_mtiles / G, G, T, order_gu, L);
-  order_pass(tp2id, b2e, B, n_mtiles, 1, T, order_dn, L);
+  for (int mt = threadIdx.x; mt < n_mtiles; mt += kOrderThreads) {
+    s_w[mt] = (uint8_t)tile_weight(tp2id, mt, T);
+    s_e[mt] = b2e[(size_t)mt * kPM / B];
+  }
+  __syncthreads();
+  order_pass(s_w, s_e, n_mtiles / G, G, order_gu, L);
+  order_pass(s_w, s_e, n_mtiles, 1, order_dn, L);
 }
 
 // inv[t, e] = slot of (t, e) or -1.
@@ -709,6 +724,9 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
                 "moe_cte: unsupported scale mode %d", scale_mode);
   const int64_t n_slots = n_blocks * block_size;
+  MXMOE_REQUIRE(n_slots / kPM <= kOrderMaxTiles,
+                "moe_cte: %lld slots exceed the %d M-tiles of 128 slots one call schedules",
+                (long long)n_slots, kOrderMaxTiles);
   const size_t need = cte_carve(nullptr, ~(size_t)0, T, H, I, E, n_slots, nullptr);
   if (workspace_bytes < need)
     return set_error(MXMOE_E_WORKSPACE, "moe_cte: workspace %zu < %zu", workspace_bytes, need);
@@ -743,9 +761,9 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
-  hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
-                     token_position_to_id, block_to_expert, (int)block_size, a.n_mtiles, a.group,
-                     (int)T, w.order_gu, w.order_dn);
+  hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
+                     (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
+                     (int)block_size, a.n_mtiles, a.group, (int)T, w.order_gu, w.order_dn);
   mark(0);
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);

@@ -33,14 +33,18 @@ __device__ __forceinline__ void for_row_quarter(const float* __restrict__ row, i
   }
 }
 
-// Pass 1: per-chunk expert masks and counts, and the masked affinities.
-// counts are stored expert-major: counts[e * n_chunks + c].
+// Pass 1: per-chunk expert masks and counts, and the masked affinities; the workgroups
+// also fill token_position_to_id with -1 (the scatter, two kernels later, writes the
+// real slots).  counts are stored expert-major: counts[e * n_chunks + c].
 __global__ void __launch_bounds__(kBwThreads) bw_count_kernel(
     const float* __restrict__ aff, const uint8_t* __restrict__ pmask, int T, int E,
     int n_chunks, float* __restrict__ aff_masked, int32_t* __restrict__ counts,
-    unsigned long long* __restrict__ chunk_masks) {
+    unsigned long long* __restrict__ chunk_masks, int32_t* __restrict__ tp2id,
+    int64_t n_slots) {
   extern __shared__ unsigned long long masks[];  // [E]
   const int tid = threadIdx.x, tl = tid >> 2, q = tid & 3, c = blockIdx.x;
+  for (int64_t i = (int64_t)c * kBwThreads + tid; i < n_slots; i += (int64_t)n_chunks * kBwThreads)
+    tp2id[i] = -1;
   for (int i = tid; i < E; i += kBwThreads) masks[i] = 0ull;
   __syncthreads();
   const int t = c * kChunkTok + tl;
@@ -128,7 +132,7 @@ __global__ void __launch_bounds__(1024) bw_scan_kernel(
   }
 }
 
-// Pass 3: scatter token ids.  token_position_to_id was filled with -1 beforehand.
+// Pass 3: scatter token ids.  token_position_to_id was filled with -1 by pass 1.
 __global__ void __launch_bounds__(kBwThreads) bw_scatter_kernel(
     const float* __restrict__ aff, int T, int E, int n_chunks,
     const int32_t* __restrict__ prefix, const unsigned long long* __restrict__ chunk_masks,
@@ -144,11 +148,6 @@ __global__ void __launch_bounds__(kBwThreads) bw_scatter_kernel(
     const int64_t pos = (int64_t)expert_pos[e] + rank;
     if (pos < n_slots) tp2id[pos] = t;
   });
-}
-
-__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 }  // namespace mxmoe
@@ -193,12 +192,10 @@ extern "C" int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* p
   int32_t* expert_pos = cv.take<int32_t>(E);
   hipStream_t s = as_stream(stream);
   const int64_t n_slots = n_blocks * block_size;
-  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
-                     token_position_to_id, n_slots, -1);
   const size_t lds = (size_t)E * sizeof(unsigned long long);
   hipLaunchKernelGGL(bw_count_kernel, dim3((unsigned)nch), dim3(kBwThreads), lds, s, affinities,
                      padding_mask, (int)T, (int)E, (int)nch, affinities_masked, counts,
-                     chunk_masks);
+                     chunk_masks, token_position_to_id, n_slots);
   hipLaunchKernelGGL(bw_scan_kernel, dim3(1), dim3(1024), 0, s, counts, (int)nch, (int)E,
                      (int)block_size, (int)n_blocks, expert_pos, block_to_expert, conditions,
                      expert_counts);
