@@ -1,18 +1,22 @@
 // Prefill (context encoding) expert MLP over the blockwise mapping.
 //
 // Both projections run the same grouped GEMM:
-//   workgroup tile = 128 slots (M) x 512 weight rows (N, 32 row groups) over all of K in
-//   128-wide chunks; 8 waves, wave w owns row groups 4w..4w+3 (64 rows = 2 gate/up
-//   pairs) against all 128 slots (up to 8 MFMA 16x16x32 tiles of 16 slots).
+//   workgroup tile = 128 slots (M) x 256 weight rows (N, 16 row groups) over all of K in
+//   128-wide chunks; 4 waves, wave w owns row groups 4w..4w+3 (64 rows = 2 gate/up
+//   pairs) against all 128 slots (up to 8 MFMA 16x16x32 tiles of 16 slots).  Two
+//   workgroups share a CU (66 KB of LDS each, two waves per SIMD), so one computes
+//   while the other waits at its barrier, loads its first chunks or stores its tile.
 //   Weights bypass LDS: each wave streams its own rows global -> registers through a
 //   ring of two chunks (the packed layout is MFMA operand order) and dequantizes them
 //   once, with the CDNA4 scaled conversion, right before its MFMAs.
 //   Activations are shared: the 128 slots' rows of a chunk (32 KiB of bf16, 16-byte
 //   blocks XOR-swizzled by row against bank conflicts) go global -> LDS by direct
-//   loads into a ring of four stages, three chunks ahead.  One s_barrier per chunk,
+//   loads into a ring of two stages, one chunk ahead.  One s_barrier per chunk,
 //   preceded by a wait for the wave's own direct loads of the chunk about to be read
 //   only (a counted vmcnt, not the full drain of __syncthreads), keeps the weight and
-//   activation streams in flight across chunks.
+//   activation streams in flight across chunks.  (The ring depth, the waves and row
+//   groups per workgroup are the constants kPStages, kPWaves and kPRG below; four
+//   stages of 512-row tiles with 8 waves, one workgroup per CU, measured 3 % slower.)
 //   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one expert;
 //   tiles whose 128 slots are all padding exit at once, and the waves run only the
 //   16-slot tiles up to the last one holding a real slot (rounded to 1, 2, 4 or 8).
@@ -20,8 +24,9 @@
 //   XCD's CUs take its workgroups in order.  M-tiles are scheduled in groups (the tiles
 //   of one block: 2 at block size 256).  XCD x runs group ranks x, x+8, x+16, ..., each
 //   as group x n_ntiles consecutive workgroups, M-tile by M-tile (the workgroups sharing
-//   activations or weight rows sit on one L2 at about the same time), where rank r is the r-th group in an order computed on the device
-//   from token_position_to_id: most 16-slot subtiles first, all-padding groups last.
+//   activations or weight rows sit on one L2 at about the same time), where rank r is
+//   the r-th group in an order computed on the device from token_position_to_id: most
+//   16-slot subtiles first, all-padding groups last.
 //   Every XCD gets an equal share of each group size, and the long groups start first
 //   (a block of 256 slots holding ~130 tokens is one full tile and one nearly empty
 //   one; in M order the empty tail blocks of the mapping would all land on the last
@@ -42,13 +47,14 @@
 namespace mxmoe {
 
 constexpr int kPM = 128;      // slots per M-tile
-constexpr int kPRG = 32;      // row groups per N-tile (512 rows)
-constexpr int kPWaves = 8;
+constexpr int kPRG = 16;      // row groups per N-tile (256 rows)
+constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kPRGW = kPRG / kPWaves;         // row groups per wave (whole scale quads)
 constexpr int kPDma = kPM / kPWaves / 4;      // direct loads (1 KiB = 4 rows) per wave and chunk
 static_assert(kPRGW == 4 || kPRGW == 8, "a wave holds one or two quads of row groups");
-constexpr int kPStages = 4;   // activation chunks in LDS
+constexpr int kPStages = 2;   // activation chunks in LDS (2 or 4)
+constexpr int kPLead = kPStages - 1;  // chunks the direct loads run ahead
 
 struct PrefillArgs {
   const uint16_t* a;      // x [T, H] (gate_up) or h [slots, I] (down)
@@ -129,7 +135,8 @@ using StageC = std::integral_constant<int, S>;
 // kPDma x 1 KiB (rows (kPM / kPWaves) w + 4i + lane / 16).  The lane's LDS slot
 // (lane % 16) of row r holds
 // column block (lane % 16) ^ (r % 16); columns past K read column 0 of the row.  Issued
-// from inline assembly (M0 = the 1 KiB's LDS address, 16 B per lane): the compiler then
+// from inline assembly (M0 = the 1 KiB's LDS address, 16 B per lane, a 32-bit offset
+// from the activations' base in a scalar register pair): the compiler then
 // keeps no account of them, which it could only settle, across the loop, with a full
 // drain before the stage's first LDS read; the counted barrier waits for them instead.
 __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c) {
@@ -139,11 +146,11 @@ __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, i
     const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
     const int kcol = c * 128 + swz * 8;
     const uint32_t off = p.a_off[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
-    const char* src = p.a + off;
     uint8_t* dst = sa + ((kPM / kPWaves) * wave + 4 * i) * 256;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+                 "s"(p.a)
                  : "memory", "m0");
   }
 }
@@ -165,14 +172,16 @@ __device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p
 #pragma unroll
   for (int r = 0; r < kPRGW; ++r) {
     const uint32_t rr = r < p.rv ? r : p.rv - 1;
-    const uint8_t* src = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u + lo * 16u;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(f.w[r]) : "v"(src) : "memory");
+    const uint8_t* base = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u;
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(f.w[r]) : "v"(lo * 16u), "s"(base)
+                 : "memory");
   }
 #pragma unroll
   for (int h = 0; h < kPRGW / 4; ++h) {
     const uint32_t qq = 4 * h < p.rv ? h : 0;
-    const uint8_t* ssrc = p.ws + qq * (uint32_t)(2 * p.K) + (uint32_t)c * 256u + lo * 4u;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(f.s[h]) : "v"(ssrc) : "memory");
+    const uint8_t* sbase = p.ws + qq * (uint32_t)(2 * p.K) + (uint32_t)c * 256u;
+    asm volatile("global_load_dword %0, %1, %2" : "=v"(f.s[h]) : "v"(lo * 4u), "s"(sbase)
+                 : "memory");
   }
 }
 
@@ -235,29 +244,32 @@ __device__ __forceinline__ void prefill_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// One chunk: chunk c is in stage S.  Issue order (the vmcnt arithmetic depends on it),
-// with D = kPDma direct loads and L = kPRGW + kPRGW / 4 weight and scale loads per chunk:
-// prologue: weights of chunks 0 and 1 (2 x L), direct loads of chunks 0, 1, 2 (3 x D);
-// step c: [barrier] direct loads of chunk c + 3 (D), [wait] the MFMAs of chunk c, the
+// One chunk: chunk c is in stage S % kPStages.  Issue order (the vmcnt arithmetic
+// depends on it), with D = kPDma direct loads and L = kPRGW + kPRGW / 4 weight and
+// scale loads per chunk and P = kPLead:
+// prologue: weights of chunks 0 and 1 (2 x L), direct loads of chunks 0 .. P - 1 (P x D);
+// step c: [barrier] direct loads of chunk c + P (D), [wait] the MFMAs of chunk c, the
 // weights of chunk c + 2 (L).
-//  - barrier: chunk c's direct loads have landed once at most 2D later loads are
-//    outstanding at step 0 and 2D + L at later steps (exactly that at step 1, more
-//    later: the wait then also covers loads two or more steps old); a wave without
-//    weights issues direct loads only: 2D at every step;
+//  - barrier: chunk c's direct loads have landed once at most (P - 1) D later loads are
+//    outstanding at step 0 and (P - 1) D + L at later steps (exactly that at step 1,
+//    more later: the wait then also covers older loads); a wave without weights issues
+//    direct loads only: (P - 1) D at every step;
 //  - weights of chunk c: at most 2D + L later loads outstanding (exactly that from step
 //    2 on; steps 0 and 1 wait a little longer, once).
-constexpr int kPWaitFirst = 2 * kPDma;
-constexpr int kPWait = 2 * kPDma + kPRGW + kPRGW / 4;
+constexpr int kPLoadsB = kPRGW + kPRGW / 4;
+constexpr int kPWaitFirst = (kPLead - 1) * kPDma;
+constexpr int kPWait = (kPLead - 1) * kPDma + kPLoadsB;
+constexpr int kPWaitB = 2 * kPDma + kPLoadsB;
 template <int S, int NT, bool ACTIVE, bool FIRST, typename Stage>
 __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
                                              const PrefillTile& p, int c,
                                              f32x4 (&acc)[kPRGW][NT]) {
   prefill_barrier<(FIRST || !ACTIVE) ? kPWaitFirst : kPWait>();
-  prefill_dma(stage(StageC<(S + 3) % kPStages>()), p, min(c + 3, p.nc - 1));
+  prefill_dma(stage(StageC<(S + kPLead) % kPStages>()), p, min(c + kPLead, p.nc - 1));
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
-    prefill_wait_b<kPWait>(f[S % 2]);
-    prefill_compute<NT>(stage(StageC<S>()), f[S % 2], p, c, acc);
+    prefill_wait_b<kPWaitB>(f[S % 2]);
+    prefill_compute<NT>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
     prefill_load_b(f[S % 2], p, min(c + 2, p.nc - 1));
     __builtin_amdgcn_sched_barrier(0);
@@ -274,8 +286,8 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
   }
   __builtin_amdgcn_sched_barrier(0);
   prefill_dma(stage(StageC<0>()), p, 0);
-  prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1));
-  prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1));
+  if constexpr (kPLead > 1) prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1));
+  if constexpr (kPLead > 2) prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1));
   __builtin_amdgcn_sched_barrier(0);
   prefill_step<0, NT, ACTIVE, true>(stage, f, p, 0, acc);
   int c = 1;
@@ -397,10 +409,11 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArg
 
 template <bool GATE_UP>
 __global__ void __launch_bounds__(kPThreads)
-    __attribute__((amdgpu_waves_per_eu(kPWaves / 4, kPWaves / 4))) prefill_gemm_kernel(
+    __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_kernel(
         PrefillArgs args) {
+  constexpr int kS23 = kPStages == 4 ? kPM * 256 : 16;  // stages 2 and 3 exist with 4 stages
   __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
-      sa2[kPM * 256], sa3[kPM * 256];
+      sa2[kS23], sa3[kS23];
   __shared__ int32_t stok[kPM];
   __shared__ int s_lastw[kPM / 64];  // per wave of slots: last slot holding a real token, or -1
   auto stage = [&](auto s_c) -> uint8_t* {
