@@ -496,10 +496,10 @@ __global__ void __launch_bounds__(kPThreads)
     prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
 }
 
-// The gate_up GEMM schedules M-tiles in groups of G consecutive tiles of one block (G =
-// the largest power of two up to 16 dividing B / 128): the group's workgroups run one
-// after another on one XCD, so a block's second, mostly empty M-tile reads the weight
-// rows while the first one's workgroups hold them in L2.
+// The GEMMs schedule M-tiles in groups of G consecutive tiles of one block (G = the
+// largest power of two up to 16 dividing B / 128): the group's workgroups run one after
+// another on one XCD, so a block's second, mostly empty M-tile reads the weight rows
+// while the first one's workgroups hold them in L2.
 constexpr int kMaxGroupTiles = 16;
 inline int prefill_group_tiles(int64_t block_size) {
   const int64_t per = block_size / kPM;
@@ -585,11 +585,11 @@ __device__ void order_pass(const uint8_t* s_w, const int32_t* s_e, int n_groups,
   }
 }
 
-// Two orders: groups of G M-tiles for the gate_up GEMM, single M-tiles for the down GEMM.
-// The tiles' weights and experts are read once into LDS (dynamic: 5 B per tile).
+// The order of the groups of G M-tiles both GEMMs run.  The tiles' weights and experts
+// are read once into LDS (dynamic: 5 B per tile).
 __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
     const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int n_mtiles,
-    int G, int T, int2* __restrict__ order_gu, int2* __restrict__ order_dn) {
+    int G, int T, int2* __restrict__ order) {
   extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
   int32_t* s_e = reinterpret_cast<int32_t*>(order_dyn);
   uint8_t* s_w = order_dyn + 4 * (size_t)n_mtiles;
@@ -599,8 +599,7 @@ __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
     s_e[mt] = b2e[(size_t)mt * kPM / B];
   }
   __syncthreads();
-  order_pass(s_w, s_e, n_mtiles / G, G, order_gu, L);
-  order_pass(s_w, s_e, n_mtiles, 1, order_dn, L);
+  order_pass(s_w, s_e, n_mtiles / G, G, order, L);
 }
 
 // inv[t, e] = slot of (t, e) or -1.
@@ -688,8 +687,7 @@ struct CteWs {
   uint16_t* h;
   uint16_t* y;
   int32_t* inv;
-  int2* order_gu;
-  int2* order_dn;
+  int2* order;
 };
 
 static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
@@ -699,8 +697,7 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   c.h = cv.take<uint16_t>(n_slots * I);
   c.y = cv.take<uint16_t>(n_slots * H);
   c.inv = cv.take<int32_t>(T * E);
-  c.order_gu = cv.take<int2>(n_slots / kPM);
-  c.order_dn = cv.take<int2>(n_slots / kPM);
+  c.order = cv.take<int2>(n_slots / kPM);
   if (w) *w = c;
   return cv.off + 256;
 }
@@ -758,7 +755,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.B = (int)block_size;
   a.n_mtiles = (int)(n_slots / kPM);
   a.group = prefill_group_tiles(block_size);
-  a.order = w.order_gu;
+  a.order = w.order;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
@@ -776,7 +773,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
   hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
                      (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
-                     (int)block_size, a.n_mtiles, a.group, (int)T, w.order_gu, w.order_dn);
+                     (int)block_size, a.n_mtiles, a.group, (int)T, w.order);
   mark(0);
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);
@@ -790,10 +787,6 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)I;
   a.N_rows = (int)H;
   a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
-  // Single M-tiles: at H = 2880 a tile has 6 N-tiles, and a group's run of full-tile
-  // workgroups then lands unevenly on an XCD's 4 shader engines (measured slower).
-  a.group = 1;
-  a.order = w.order_dn;
   hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);
   mark(2);
