@@ -158,8 +158,10 @@ int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64
                 "router: unknown activation %d", act);
   if (T == 0) return MXMOE_OK;
   if (T >= 1024 && E >= 64) {
-    dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
-    hipLaunchKernelGGL((router_logits_kernel<4, 4>), grid, dim3(256), 0, s, x, w, bias, logits,
+    // 32 tokens x 64 experts per workgroup: 256 workgroups at 4096 tokens and 128 experts
+    // (64 x 64 tiles left half of the CUs idle: 34 -> 27 us with the top-k).
+    dim3 grid((unsigned)((T + 31) / 32), (unsigned)((E + 63) / 64));
+    hipLaunchKernelGGL((router_logits_kernel<2, 4>), grid, dim3(256), 0, s, x, w, bias, logits,
                        (int)T, (int)H, (int)E);
   } else {
     dim3 grid((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16));
