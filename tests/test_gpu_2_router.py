@@ -41,7 +41,8 @@ def compare_routing(aff_g, logits_g, aff_r, logits_r, k):
 
 @pytest.mark.parametrize("T,E,k,H", [(1, 32, 4, 2880), (64, 128, 4, 2880), (4096, 32, 4, 2880),
                                      (4096, 128, 4, 2880), (128, 256, 8, 7168), (17, 8, 2, 64),
-                                     (64, 512, 4, 256), (33, 300, 8, 128), (1000, 1024, 8, 256)])
+                                     (64, 512, 4, 256), (33, 300, 8, 128), (1000, 1024, 8, 256),
+                                     (1030, 100, 4, 256)])
 def test_router_softmax(dev, T, E, k, H):
     from vllm_neuron_amd import functional as NF
 
