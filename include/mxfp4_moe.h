@@ -191,6 +191,27 @@ int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w, const uint16_t
                      void* stream);
 
 /*
+ * The decode MoE block in one call: RMSNorm (as mxmoe_rmsnorm: variance over the first
+ * h_actual columns, bf16 result, columns past h_actual zero) into the workspace, then
+ * mxmoe_moe_decode on the normalized rows.  Replaces the RMSNorm + router + expert
+ * stages of nkilib moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512;
+ * semantics of :134-297) for one expert-parallel rank holding every expert.
+ * x bf16 [T, H] (not normalized); gamma fp32 [H]; the rest as mxmoe_moe_decode.
+ * stage_events: NULL, or 7 hipEvent_t: before the RMSNorm, then the 6 of
+ * mxmoe_moe_decode.
+ */
+size_t mxmoe_moe_block_decode_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                              int top_k);
+int mxmoe_moe_block_decode(const uint16_t* x, const float* gamma, int64_t h_actual, float eps,
+                           const uint16_t* router_w, const uint16_t* router_b, int router_act,
+                           int act_before_topk, int renorm, float renorm_eps, const uint8_t* gu_q,
+                           const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
+                           const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H,
+                           int64_t I, int64_t E, int top_k, int act, const float* clamps,
+                           int scale_mode, uint16_t* out, float* logits_out, void* workspace,
+                           size_t workspace_bytes, void* const* stage_events, void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour
  * the kernels rely on.  mxmoe_probe_hw_dequant runs the CDNA4 scaled fp4->bf16
  * conversion the GEMMs use over blocks/scales like mxmoe_dequant_bf16;

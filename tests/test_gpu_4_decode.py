@@ -187,6 +187,67 @@ def test_moe_block_tkg_api(dev):
     check_close(out.cpu(), want, None, "moe_block_tkg")
 
 
+@pytest.mark.parametrize("T,act,pre_norm,renorm,ha", [(64, "SIGMOID", True, True, 2800),
+                                                      (40, "SOFTMAX", False, False, None)])
+def test_moe_block_tkg_api_norm_and_router_options(dev, T, act, pre_norm, renorm, ha):
+    """The one-call block path (RMSNorm with a random gamma over the first ha columns,
+    router options, experts) against the oracle's RMSNorm + router and routed layer."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import moe_block_tkg as obt
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 8, dev, E=32)
+    x = synthetic.tokens(28, T, ref.H)
+    gamma = 1.0 + 0.1 * torch.randn(ref.H, generator=torch.Generator().manual_seed(3))
+    w = layer.w
+    rw = ref.router_w.T.contiguous().to(dev)
+    args = dict(top_k=4, expert_gate_up_weights_scale=w.gu_s, expert_down_weights_scale=w.dn_s,
+                expert_gate_up_bias=w.gu_bias, expert_down_bias=w.dn_bias, router_act_fn=act,
+                router_pre_norm=pre_norm, norm_topk_prob=renorm,
+                expert_affinities_scaling_mode="POST_SCALE", hidden_act_fn="Swish",
+                hidden_actual=ha, **ref.clamps)
+    out, logits = NF.moe_block_tkg(x.to(dev), gamma.to(dev), rw, w.gu_q, w.dn_q, **args)
+    out2, _ = NF.moe_block_tkg(x.to(dev), gamma.to(dev), rw, w.gu_q, w.dn_q, **args)
+    assert torch.equal(out, out2)  # the cached transposed router weights give the same result
+    xn, logits_r, top, idx = obt.rmsnorm_router(x, gamma, ref.router_w.T, None, 1e-6, 4, act,
+                                                pre_norm, renorm, ha)
+    assert torch.allclose(logits.cpu(), logits_r, rtol=1e-4, atol=1e-4)
+    aff = torch.zeros(T, ref.E).scatter_(1, idx, top)
+    want = ref.decode_routed(xn, aff)
+    check_close(out.cpu(), want, None, f"moe_block_tkg {act} pre_norm={pre_norm} ha={ha}")
+
+
+def test_moe_block_tkg_api_expert_slice(dev):
+    """A rank holding 16 of 32 experts (rank_id 1): RMSNorm, router over all 32, local
+    ids, experts of the slice."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.weights import MXFP4Experts
+
+    from oracle import moe_block_tkg as obt
+
+    ref, layer, lt = build(synthetic.GPT_OSS_20B, 9, dev, E=32)
+    T = 16
+    x = synthetic.tokens(29, T, ref.H)
+    gamma = torch.ones(ref.H)
+    w = MXFP4Experts.from_checkpoint(lt.gate_up_blocks[16:], lt.gate_up_scales[16:],
+                                     lt.down_blocks[16:], lt.down_scales[16:],
+                                     lt.gate_up_bias[16:], lt.down_bias[16:]).to(dev)
+    out, _ = NF.moe_block_tkg(
+        x.to(dev), gamma.to(dev), ref.router_w.T.contiguous().to(dev), w.gu_q, w.dn_q,
+        rank_id=torch.tensor([1], device=dev), top_k=4, expert_gate_up_weights_scale=w.gu_s,
+        expert_down_weights_scale=w.dn_s, expert_gate_up_bias=w.gu_bias,
+        expert_down_bias=w.dn_bias, router_act_fn="SOFTMAX", router_pre_norm=False,
+        expert_affinities_scaling_mode="POST_SCALE", hidden_act_fn="Swish", **ref.clamps)
+    xn, _, top, idx = obt.rmsnorm_router(x, gamma, ref.router_w.T, None, 1e-6, 4, "SOFTMAX",
+                                         False, False)
+    aff = torch.zeros(T, ref.E).scatter_(1, idx, top)
+    aff[:, :16] = 0.0
+    want = ref.decode_routed(xn, aff)
+    check_close(out.cpu(), want, None, "moe_block_tkg expert slice")
+
+
 def test_decode_gptoss120b_t64_sample(dev):
     """120B-shaped layer (128 experts) at 64 tokens: a sample of 8 tokens against the
     oracle (per-token outputs depend only on the token's own row and routing)."""

@@ -46,6 +46,10 @@ _SIGNATURES = {
     "mxmoe_moe_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_decode": (_I, [_P, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                               _I64, _I, _I, _P, _I, _P, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_block_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
+    "mxmoe_moe_block_decode": (_I, [_P, _P, _I64, _F, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P,
+                                    _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I, _P, _P, _P, _SZ,
+                                    _P, _P]),
     "mxmoe_probe_hw_dequant": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_probe_mfma": (_I, [_P, _P, _P, _P]),
 }

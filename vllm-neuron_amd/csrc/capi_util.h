@@ -35,6 +35,10 @@ int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64
                float* logits, float* affinities, int32_t* topk_idx, float* topk_val,
                hipStream_t s);
 
+// RMSNorm over the first ha columns of each row, bf16 out (router.hip).
+int rmsnorm_run(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t ha,
+                float eps, uint16_t* out, hipStream_t s);
+
 // Bump allocator over a caller-provided workspace.
 struct Carver {
   char* base;

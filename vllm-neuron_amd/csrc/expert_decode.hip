@@ -831,3 +831,34 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
                       top_k, act, clamps, scale_mode, out, w,
                       stage_events ? stage_events + 1 : nullptr, s);
 }
+
+extern "C" size_t mxmoe_moe_block_decode_workspace_bytes(int64_t T, int64_t H, int64_t I,
+                                                         int64_t E, int top_k) {
+  return align_up(mxmoe_moe_decode_workspace_bytes(T, H, I, E, top_k), 256) +
+         align_up((size_t)T * (size_t)H * 2u, 256);
+}
+
+extern "C" int mxmoe_moe_block_decode(
+    const uint16_t* x, const float* gamma, int64_t h_actual, float eps, const uint16_t* router_w,
+    const uint16_t* router_b, int router_act, int act_before_topk, int renorm, float renorm_eps,
+    const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
+    const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
+    int top_k, int act, const float* clamps, int scale_mode, uint16_t* out, float* logits_out,
+    void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream) {
+  clear_error();
+  MXMOE_REQUIRE(x && gamma && workspace, "moe_block_decode: null pointer");
+  const size_t need = mxmoe_moe_block_decode_workspace_bytes(T, H, I, E, top_k);
+  if (workspace_bytes < need)
+    return set_error(MXMOE_E_WORKSPACE, "moe_block_decode: workspace %zu < %zu", workspace_bytes,
+                     need);
+  const size_t dec = align_up(mxmoe_moe_decode_workspace_bytes(T, H, I, E, top_k), 256);
+  uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + dec);
+  hipStream_t s = as_stream(stream);
+  mark_event(stage_events, 0, s);
+  int rc = rmsnorm_run(x, gamma, T, H, h_actual, eps, xn, s);
+  if (rc) return rc;
+  return mxmoe_moe_decode(xn, router_w, router_b, router_act, act_before_topk, renorm, renorm_eps,
+                          gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E, top_k, act, clamps,
+                          scale_mode, out, logits_out, workspace, dec,
+                          stage_events ? stage_events + 1 : nullptr, stream);
+}

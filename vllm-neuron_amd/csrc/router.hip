@@ -201,13 +201,22 @@ extern "C" int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uin
                     affinities, topk_idx, topk_val, as_stream(stream));
 }
 
+namespace mxmoe {
+
+int rmsnorm_run(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t ha,
+                float eps, uint16_t* out, hipStream_t s) {
+  MXMOE_REQUIRE(x && gamma && out, "rmsnorm: null pointer");
+  MXMOE_REQUIRE(T >= 0 && H > 0 && ha > 0 && ha <= H, "rmsnorm: bad shape");
+  if (T == 0) return MXMOE_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)T), dim3(256), 0, s, x, gamma, (int)H,
+                     (int)ha, eps, out);
+  return check_launch("rmsnorm");
+}
+
+}  // namespace mxmoe
+
 extern "C" int mxmoe_rmsnorm(const uint16_t* x, const float* gamma, int64_t T, int64_t H,
                              int64_t h_actual, float eps, uint16_t* out, void* stream) {
   clear_error();
-  MXMOE_REQUIRE(x && gamma && out, "rmsnorm: null pointer");
-  MXMOE_REQUIRE(T >= 0 && H > 0 && h_actual > 0 && h_actual <= H, "rmsnorm: bad shape");
-  if (T == 0) return MXMOE_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)T), dim3(256), 0, as_stream(stream), x, gamma,
-                     (int)H, (int)h_actual, eps, out);
-  return check_launch("rmsnorm");
+  return rmsnorm_run(x, gamma, T, H, h_actual, eps, out, as_stream(stream));
 }

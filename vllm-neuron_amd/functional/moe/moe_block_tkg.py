@@ -2,11 +2,13 @@
 
 Mirrors vllm_neuron/functional/moe/moe_block_tkg.py:305-571 (signature, defaults,
 exception types).  The reference runs nkilib moe_block_tkg (:469-517) or its torch
-flow ``_torch_moe_block_tkg_impl`` (:56-302); here: mxmoe_rmsnorm (variance over
-the first ``hidden_actual`` columns, result cast to the input dtype as :134-150),
-mxmoe_router_topk on the normalized rows (fp32 logits, router_pre_norm /
-norm_topk_prob as :152-204), then mxmoe_moe_tkg (fp32 expert math over the
-selected experts, ascending-id fp32 sum, cast to the input dtype).
+flow ``_torch_moe_block_tkg_impl`` (:56-302); here, with every expert on the rank,
+one mxmoe_moe_block_decode call: RMSNorm (variance over the first ``hidden_actual``
+columns, result cast to the input dtype as :134-150), the router on the normalized
+rows (fp32 logits, router_pre_norm / norm_topk_prob as :152-204), then the experts (fp32
+expert math over the selected experts, ascending-id fp32 sum, cast to the input dtype).
+With a slice of the experts (rank_id), the same steps as mxmoe_rmsnorm,
+mxmoe_router_topk and mxmoe_moe_tkg on the local expert ids.
 
 Shared experts, fused residual add and activation quantization have no MI355X
 kernel and raise NotImplementedError, like the reference's torch flow does for
@@ -40,6 +42,56 @@ def rmsnorm(x: Tensor, gamma: Tensor, eps: float, hidden_actual: Optional[int] =
                                   out.data_ptr(), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_rmsnorm")
     return out
+
+
+# The router weights arrive as [H, E] (the reference's layout); the kernels read [E, H].
+# The transposed copy is kept per (storage, version, shape, strides), so a weight tensor
+# passed at every decode step is transposed once (an in-place update bumps its version).
+_ROUTER_T: "dict" = {}
+_ROUTER_T_MAX = 256
+
+
+def _router_eh(router_weights: Tensor) -> Tensor:
+    key = (router_weights.data_ptr(), router_weights._version, tuple(router_weights.shape),
+           tuple(router_weights.stride()), str(router_weights.device))
+    w = _ROUTER_T.get(key)
+    if w is None:
+        if len(_ROUTER_T) >= _ROUTER_T_MAX:
+            _ROUTER_T.clear()
+        w = router_weights.t().contiguous()
+        _ROUTER_T[key] = w
+    return w
+
+
+def _block_decode(x, gamma, eps, hidden_actual, router_weights, bias, act, pre_norm, renorm,
+                  top_k, gu_q, gu_s, dn_q, dn_s, gub, dnb, hidden_act, clamps, scale_mode,
+                  want_logits):
+    """mxmoe_moe_block_decode: x bf16 [T, H] (not normalized), router_weights [H, E]."""
+    dev = _lib.require_cuda(x, gamma, router_weights, gu_q)
+    E, H, I = expert_shapes(gu_q, gu_s, dn_q, dn_s)
+    T = x.shape[0]
+    ha = H if hidden_actual is None else int(hidden_actual)
+    g = gamma.reshape(-1).to(torch.float32).contiguous()
+    if g.numel() != H:
+        raise ValueError(f"gamma has {g.numel()} elements, expected {H}")
+    if x.shape[1] != H:
+        raise ValueError(f"hidden states have {x.shape[1]} columns, the experts {H}")
+    w_eh = _router_eh(router_weights)
+    if bias is not None:
+        bias = bias.contiguous()
+    x = x.contiguous()
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev) if want_logits else None
+    L = _lib.lib()
+    ws = _lib.workspace(L.mxmoe_moe_block_decode_workspace_bytes(T, H, I, E, top_k), dev)
+    rc = L.mxmoe_moe_block_decode(
+        x.data_ptr(), g.data_ptr(), ha, float(eps), w_eh.data_ptr(), _lib.ptr(bias), act,
+        int(pre_norm), int(renorm), 1e-20, gu_q.data_ptr(), gu_s.data_ptr(), dn_q.data_ptr(),
+        dn_s.data_ptr(), _lib.ptr(gub), _lib.ptr(dnb), T, H, I, E, top_k, hidden_act, clamps,
+        scale_mode, out.data_ptr(), _lib.ptr(logits), ws.data_ptr(), ws.numel(), None,
+        _lib.stream_handle(dev))
+    _lib.check(rc, "mxmoe_moe_block_decode")
+    return out, logits
 
 
 def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
@@ -95,12 +147,27 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
         raise NotImplementedError("router_weights must be bfloat16")
     if router_bias is not None and router_bias.dtype != torch.bfloat16:
         raise NotImplementedError("router_bias must be bfloat16")
+    E_g = router_weights.shape[1]
+    bias = None if router_bias is None else router_bias.reshape(-1)
+    if E_L == E_g:
+        # Every expert on this rank: RMSNorm, router and experts in one library call.
+        out, logits = _block_decode(inp, gamma, eps, hidden_actual, router_weights, bias, act,
+                                    bool(router_pre_norm), bool(norm_topk_prob), top_k,
+                                    expert_gate_up_weights, expert_gate_up_weights_scale,
+                                    expert_down_weights, expert_down_weights_scale,
+                                    gate_up_bias(expert_gate_up_bias, E_L, I),
+                                    down_bias(expert_down_bias, E_L, H), act_code(hidden_act_fn),
+                                    _lib.clamps_array(gate_clamp_lower_limit,
+                                                      gate_clamp_upper_limit,
+                                                      up_clamp_lower_limit,
+                                                      up_clamp_upper_limit),
+                                    scale_code(expert_affinities_scaling_mode),
+                                    not skip_router_logits)
+        return out if skip_router_logits else (out, logits)
     xn = rmsnorm(inp, gamma, eps, hidden_actual)
     w_eh = router_weights.t()
-    bias = None if router_bias is None else router_bias.reshape(-1)
     _, logits, idx, val = router_topk_raw(xn, w_eh, top_k, bias, act, bool(router_pre_norm),
                                           bool(norm_topk_prob), 1e-20)
-    E_g = router_weights.shape[1]
     if E_L < E_g and rank_id is not None:
         idx = idx - E_L * rank_id.reshape(-1)[0].to(idx.dtype)
     out = moe_tkg_raw(xn, idx, val, expert_gate_up_weights, expert_gate_up_weights_scale,
