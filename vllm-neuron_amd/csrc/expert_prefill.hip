@@ -316,16 +316,134 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
   }
 }
 
-template <bool GATE_UP, int NT, typename Stage>
-__device__ __forceinline__ void prefill_run(const Stage& stage, const PrefillArgs& args,
-                                            const PrefillTile& p, const int32_t* stok, int m0,
-                                            int e, int rg_first) {
+// Tiles with 1 or 2 subtiles of 16 slots (a block's nearly empty second tile) have little
+// to compute per chunk, so a chunk costs about one load latency.  They run a loop of their
+// own: only their 16 NT rows of activations go to LDS, in a ring of kLStages slices of the
+// 64 KB the full tiles use as two stages, kLLead chunks ahead; the weights go through a
+// ring of kLSlots register chunks (their accumulators leave the registers free), kLSlots
+// chunks ahead.  Wave w brings rows 4 (w + 4j) .. 4 (w + 4j) + 3, j < NT.
+constexpr int kLLead = 7, kLStages = 8, kLSlots = 4;
+static_assert(kLStages > kLLead && (kLStages & (kLStages - 1)) == 0, "light ring");
+
+template <int NT>
+__device__ __forceinline__ void prefill_dma_light(uint8_t* ring, int slot, const PrefillTile& p,
+                                                  int c) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+  uint8_t* sa = ring + slot * (16 * NT * 256);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int r4 = 4 * (wave + 4 * j);
+    const int swz = (lane & 15) ^ ((r4 + (lane >> 4)) & 15);
+    const int kcol = c * 128 + swz * 8;
+    const uint32_t off = p.a_off[j] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
+    uint8_t* dst = sa + r4 * 256;
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+                 "s"(p.a)
+                 : "memory", "m0");
+  }
+}
+
+// One chunk of the light loop, chunk c in slice c % kLStages and weight slot SB = c %
+// kLSlots.  Issue order: prologue: weights of chunks 0 .. kLSlots - 1 (kLSlots x L), direct
+// loads of chunks 0 .. kLLead - 1 (kLLead x D); step c: [barrier] direct loads of chunk
+// c + kLLead (D), [wait] the MFMAs of chunk c, the weights of chunk c + kLSlots (L); D = NT,
+// L = kPLoadsB (0 for a wave without weights).
+//  - barrier: chunk c's direct loads have landed once at most (kLLead - 1) D + min(c,
+//    kLLead) L later loads are outstanding (exact at every step: BAR);
+//  - weights of chunk c: at most kLSlots D + (kLSlots - 1) L (exact from step kLSlots on,
+//    a little longer before).
+template <int SB, int NT, bool ACTIVE, int BAR>
+__device__ __forceinline__ void prefill_step_light(uint8_t* ring, PrefillB (&f)[kLSlots],
+                                                   const PrefillTile& p, int c,
+                                                   f32x4 (&acc)[kPRGW][NT]) {
+  prefill_barrier<BAR>();
+  prefill_dma_light<NT>(ring, (c + kLLead) & (kLStages - 1), p, min(c + kLLead, p.nc - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ACTIVE) {
+    prefill_wait_b<kLSlots * NT + (kLSlots - 1) * kPLoadsB>(f[SB]);
+    prefill_compute<NT>(ring + (c & (kLStages - 1)) * (16 * NT * 256), f[SB], p, c, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    prefill_load_b(f[SB], p, min(c + kLSlots, p.nc - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int NT, bool ACTIVE>
+__device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillTile& p,
+                                                   f32x4 (&acc)[kPRGW][NT]) {
+  constexpr int D = NT, L = ACTIVE ? kPLoadsB : 0, B0 = (kLLead - 1) * D;
+  static_assert(B0 + kLLead * L < 64 && kLSlots * D + (kLSlots - 1) * L < 64, "vmcnt range");
+  static_assert(kLSlots == 4, "the unrolled steps below cycle through four weight slots");
+  PrefillB f[kLSlots];
+  if constexpr (ACTIVE) {
+#pragma unroll
+    for (int s = 0; s < kLSlots; ++s) prefill_load_b(f[s], p, min(s, p.nc - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int v = 0; v < kLLead; ++v) prefill_dma_light<NT>(ring, v, p, min(v, p.nc - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  // Steps 0 .. kLLead - 1 have their own barrier counts; nested, so that every path issues
+  // the loads in the order the counts assume.
+  prefill_step_light<0, NT, ACTIVE, B0>(ring, f, p, 0, acc);
+  if (1 < p.nc) {
+    prefill_step_light<1, NT, ACTIVE, B0 + L>(ring, f, p, 1, acc);
+    if (2 < p.nc) {
+      prefill_step_light<2, NT, ACTIVE, B0 + 2 * L>(ring, f, p, 2, acc);
+      if (3 < p.nc) {
+        prefill_step_light<3, NT, ACTIVE, B0 + 3 * L>(ring, f, p, 3, acc);
+        if (4 < p.nc) {
+          prefill_step_light<0, NT, ACTIVE, B0 + 4 * L>(ring, f, p, 4, acc);
+          if (5 < p.nc) {
+            prefill_step_light<1, NT, ACTIVE, B0 + 5 * L>(ring, f, p, 5, acc);
+            if (6 < p.nc) {
+              prefill_step_light<2, NT, ACTIVE, B0 + 6 * L>(ring, f, p, 6, acc);
+              constexpr int BS = B0 + kLLead * L;
+              int c = kLLead;
+              for (; c + 4 <= p.nc; c += 4) {
+                prefill_step_light<3, NT, ACTIVE, BS>(ring, f, p, c, acc);
+                prefill_step_light<0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
+                prefill_step_light<1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
+                prefill_step_light<2, NT, ACTIVE, BS>(ring, f, p, c + 3, acc);
+              }
+              if (c < p.nc) {
+                prefill_step_light<3, NT, ACTIVE, BS>(ring, f, p, c, acc);
+                if (c + 1 < p.nc) {
+                  prefill_step_light<0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
+                  if (c + 2 < p.nc) prefill_step_light<1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  // As in prefill_loop: every load has landed before the wave goes on, and the ring's
+  // registers are operands of the final wait.
+  if constexpr (ACTIVE) {
+#pragma unroll
+    for (int s = 0; s < kLSlots; ++s) prefill_wait_b<0>(f[s]);
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
+template <bool GATE_UP, int NT, bool LIGHT, typename Stage>
+__device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
+                                            const PrefillArgs& args, const PrefillTile& p,
+                                            const int32_t* stok, int m0, int e, int rg_first) {
   f32x4 acc[kPRGW][NT];
 #pragma unroll
   for (int r = 0; r < kPRGW; ++r)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  prefill_loop<NT, true>(stage, p, acc);
+  if constexpr (LIGHT)
+    prefill_loop_light<NT, true>(ring, p, acc);
+  else
+    prefill_loop<NT, true>(stage, p, acc);
 
   const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
@@ -412,14 +530,13 @@ __global__ void __launch_bounds__(kPThreads)
     __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_kernel(
         PrefillArgs args) {
   constexpr int kS23 = kPStages == 4 ? kPM * 256 : 16;  // stages 2 and 3 exist with 4 stages
-  __shared__ __attribute__((aligned(1024))) uint8_t sa0[kPM * 256], sa1[kPM * 256],
-      sa2[kS23], sa3[kS23];
+  __shared__ __attribute__((aligned(1024))) uint8_t sa01[2][kPM * 256], sa2[kS23], sa3[kS23];
   __shared__ int32_t stok[kPM];
   __shared__ int s_lastw[kPM / 64];  // per wave of slots: last slot holding a real token, or -1
   auto stage = [&](auto s_c) -> uint8_t* {
     constexpr int S = decltype(s_c)::value;
-    if constexpr (S == 0) return sa0;
-    else if constexpr (S == 1) return sa1;
+    if constexpr (S == 0) return sa01[0];
+    else if constexpr (S == 1) return sa01[1];
     else if constexpr (S == 2) return sa2;
     else return sa3;
   };
@@ -469,15 +586,39 @@ __global__ void __launch_bounds__(kPThreads)
   p.nfull = p.K / 128;
   p.tail_q = (p.K % 128) / 32;
   p.a = reinterpret_cast<const char*>(args.a);
-#pragma unroll
-  for (int i = 0; i < kPDma; ++i) {
-    const int row = (kPM / kPWaves) * wave + 4 * i + (lane >> 4);
+  // Byte offset of tile row `row`'s activations.  Padding slots read a real row (token 0 /
+  // the tile's first slot): an MFMA output column depends on its own slot only, and
+  // padding columns are never stored.
+  auto a_row_off = [&](int row) {
     const int tk = stok[row];
-    // Padding slots read a real row (token 0 / the tile's first slot): an MFMA output
-    // column depends on its own slot only, and padding columns are never stored.
-    const uint32_t arow = GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + row : m0);
-    p.a_off[i] = arow * (uint32_t)p.K * 2u;
+    const uint32_t arow =
+        GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + row : m0);
+    return arow * (uint32_t)p.K * 2u;
+  };
+  const int ntiles = last / 16 + 1;  // real slots of a block come first
+  if (ntiles <= 2) {
+    // The light loop's direct loads: rows 4 (wave + 4j) + lane / 16 of the tile.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) p.a_off[j] = a_row_off(4 * (wave + 4 * j) + (lane >> 4));
+    uint8_t* ring = &sa01[0][0];
+    if (p.rv <= 0) {
+      if (ntiles <= 1) {
+        f32x4 none[kPRGW][1];
+        prefill_loop_light<1, false>(ring, p, none);
+      } else {
+        f32x4 none[kPRGW][2];
+        prefill_loop_light<2, false>(ring, p, none);
+      }
+      return;
+    }
+    if (ntiles <= 1)
+      prefill_run<GATE_UP, 1, true>(stage, ring, args, p, stok, m0, e, rg_first);
+    else
+      prefill_run<GATE_UP, 2, true>(stage, ring, args, p, stok, m0, e, rg_first);
+    return;
   }
+#pragma unroll
+  for (int i = 0; i < kPDma; ++i) p.a_off[i] = a_row_off((kPM / kPWaves) * wave + 4 * i + (lane >> 4));
   if (p.rv <= 0) {
     // No row groups in this tile for this wave: it still brings its share of the
     // activations and meets the barriers.
@@ -485,15 +626,10 @@ __global__ void __launch_bounds__(kPThreads)
     prefill_loop<1, false>(stage, p, none);
     return;
   }
-  const int ntiles = last / 16 + 1;  // real slots of a block come first
-  if (ntiles <= 1)
-    prefill_run<GATE_UP, 1>(stage, args, p, stok, m0, e, rg_first);
-  else if (ntiles <= 2)
-    prefill_run<GATE_UP, 2>(stage, args, p, stok, m0, e, rg_first);
-  else if (ntiles <= 4)
-    prefill_run<GATE_UP, 4>(stage, args, p, stok, m0, e, rg_first);
+  if (ntiles <= 4)
+    prefill_run<GATE_UP, 4, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
   else
-    prefill_run<GATE_UP, 8>(stage, args, p, stok, m0, e, rg_first);
+    prefill_run<GATE_UP, 8, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
 }
 
 // The GEMMs schedule M-tiles in groups of G consecutive tiles of one block (G = the
