@@ -95,14 +95,17 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
-__device__ __forceinline__ float act_bf16(float g, int act) {
-  if (act == kSwish) {
+template <int ACT>
+__device__ __forceinline__ float act_bf16(float g) {
+  if constexpr (ACT == kSwish) {
     const float t1 = rb(g * 1.702f);
     const float t2 = rb(sigmoid_fast(t1));
     return rb(g * t2);
+  } else if constexpr (ACT == kSiLU) {
+    return rb(g * sigmoid_fast(g));
+  } else {
+    return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
   }
-  if (act == kSiLU) return rb(g * sigmoid_fast(g));
-  return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
 }
 
 // Per-workgroup and per-wave constants of a tile.
@@ -431,6 +434,45 @@ __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillT
   }
 }
 
+// gate_up epilogue: bias, clamps and the activation on the bf16-rounded accumulators
+// (the reference's bf16 intermediates), h = up * act(gate) stored as bf16.
+template <int ACT, int NT>
+__device__ __forceinline__ void gate_up_store(const PrefillArgs& args, const PrefillTile& p,
+                                              const f32x4 (&acc)[kPRGW][NT],
+                                              const float (&gb)[kPRGW / 2][4],
+                                              const float (&ub)[kPRGW / 2][4],
+                                              const int32_t* stok, int m0, int rg_first) {
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, q = lane >> 4;
+  const int I = args.I;
+#pragma unroll
+  for (int pp = 0; pp < kPRGW / 2; ++pp) {
+    if (2 * pp >= p.rv) continue;
+    const int P = rg_first / 2 + pp;  // pair index = 16 intermediate columns
+    const int col0 = 16 * P + 4 * q;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int row = 16 * t + (lane & 15);
+      if (stok[row] < 0) continue;
+      const f32x4 g4 = acc[2 * pp][t], u4 = acc[2 * pp + 1][t];
+      uint16_t h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g = rb(g4[i]), u = rb(u4[i]);
+        if (args.bias) {
+          g = rb(g + gb[pp][i]);
+          u = rb(u + ub[pp][i]);
+        }
+        g = clamp_ref(g, args.p.gate_lo, args.p.gate_hi);
+        u = clamp_ref(u, args.p.up_lo, args.p.up_hi);
+        h[i] = f32_to_bf16_bits(u * act_bf16<ACT>(g));
+      }
+      *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * I + col0) =
+          u16x4{h[0], h[1], h[2], h[3]};
+    }
+  }
+}
+
 template <bool GATE_UP, int NT, bool LIGHT, typename Stage>
 __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
                                             const PrefillArgs& args, const PrefillTile& p,
@@ -467,32 +509,13 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
         ub[pp][i] = bf16_bits_to_f32(bsrc[iu]);
       }
     }
-#pragma unroll
-    for (int pp = 0; pp < kPRGW / 2; ++pp) {
-      if (2 * pp >= p.rv) continue;
-      const int P = rg_first / 2 + pp;  // pair index = 16 intermediate columns
-      const int col0 = 16 * P + 4 * q;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int row = 16 * t + (lane & 15);
-        if (stok[row] < 0) continue;
-        const f32x4 g4 = acc[2 * pp][t], u4 = acc[2 * pp + 1][t];
-        uint16_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float g = rb(g4[i]), u = rb(u4[i]);
-          if (args.bias) {
-            g = rb(g + gb[pp][i]);
-            u = rb(u + ub[pp][i]);
-          }
-          g = clamp_ref(g, args.p.gate_lo, args.p.gate_hi);
-          u = clamp_ref(u, args.p.up_lo, args.p.up_hi);
-          h[i] = f32_to_bf16_bits(u * act_bf16(g, args.p.act));
-        }
-        *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * I + col0) =
-            u16x4{h[0], h[1], h[2], h[3]};
-      }
-    }
+    // The activation is uniform: one dispatch, then straight-line code per element.
+    if (args.p.act == kSwish)
+      gate_up_store<kSwish>(args, p, acc, gb, ub, stok, m0, rg_first);
+    else if (args.p.act == kSiLU)
+      gate_up_store<kSiLU>(args, p, acc, gb, ub, stok, m0, rg_first);
+    else
+      gate_up_store<kGELU>(args, p, acc, gb, ub, stok, m0, rg_first);
   } else {
     const int H = args.H;
     float bb[kPRGW][4];
