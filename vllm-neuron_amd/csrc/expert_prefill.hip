@@ -111,7 +111,9 @@ __device__ __forceinline__ float act_bf16(float g) {
 // Per-workgroup and per-wave constants of a tile.
 struct PrefillTile {
   const char* a;             // activations
-  uint32_t a_off[kPDma];     // byte offsets of this lane's source rows (padding: a real row)
+  const uint32_t* rowoff;    // LDS: byte offset of each tile row's source row (padding: a
+                             // real row), re-read at every chunk (fewer live registers)
+  uint32_t a_off[kPDma];     // the same for this lane's rows, in registers (PD = 0 loops)
   const uint8_t* wq;         // this wave's first row group
   const uint8_t* ws;         // this wave's scale quad
   uint32_t rg_bytes;
@@ -142,13 +144,25 @@ using StageC = std::integral_constant<int, S>;
 // from the activations' base in a scalar register pair): the compiler then
 // keeps no account of them, which it could only settle, across the loop, with a full
 // drain before the stage's first LDS read; the counted barrier waits for them instead.
-__device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c) {
+// The lane's source row offsets (ro): kept in registers by the loops whose fragment reads
+// the compiler schedules (PD = 0), else read from LDS before the barrier that precedes
+// the direct loads, so that their latency hides behind its wait.
+template <int PD>
+__device__ __forceinline__ void prefill_rowoffs(const PrefillTile& p, uint32_t (&ro)[kPDma]) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < kPDma; ++i)
+    ro[i] = PD == 0 ? p.a_off[i] : p.rowoff[(kPM / kPWaves) * wave + 4 * i + (lane >> 4)];
+}
+
+__device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c,
+                                            const uint32_t (&ro)[kPDma]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < kPDma; ++i) {
     const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
     const int kcol = c * 128 + swz * 8;
-    const uint32_t off = p.a_off[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
+    const uint32_t off = ro[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
     uint8_t* dst = sa + ((kPM / kPWaves) * wave + 4 * i) * 256;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
@@ -210,7 +224,7 @@ __device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
 
 // acc[r][t] += W[row group r] x A[16-slot tile t] over chunk c.  Lanes past K get a zero
 // scale, so their weights add exact zeros.
-template <int NT>
+template <int NT, int PD>
 __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const PrefillB& f,
                                                 const PrefillTile& p, int c,
                                                 f32x4 (&acc)[kPRGW][NT]) {
@@ -220,21 +234,59 @@ __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const Prefill
 #pragma unroll
   for (int r = 0; r < kPRGW; ++r)
     sc[r] = kok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
-  // Per 32-wide step: the row groups' weights dequantized once, then one activation
-  // fragment at a time against them (few registers live).
+  // Per 32-wide step j: the row groups' weights dequantized once, then the NT activation
+  // fragments against them.  The fragments are read from LDS PD steps (j, t) ahead, into
+  // a rotating set of registers, so each read has the MFMAs of PD steps to land in.
+  if constexpr (PD == 0) {
+    // Left to the compiler's schedule (it reads two fragments ahead).
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int blk = (4 * q + j) ^ (lane & 15);
+    for (int j = 0; j < 4; ++j) {
+      const int blk = (4 * q + j) ^ (lane & 15);
+      bf16x8 wf[kPRGW];
+#pragma unroll
+      for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const u32x4 xv =
+            *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
+#pragma unroll
+        for (int r = 0; r < kPRGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
+      }
+    }
+  } else {
+    constexpr int NS = 4 * NT;
+    static_assert(PD >= 1 && PD <= NS, "read-ahead distance");
+    const uint8_t* rowp = sa + (lane & 15) * 256;
+    auto frag = [&](int i) {
+      const int j = i / NT, t = i % NT;
+      const int blk = (4 * q + j) ^ (lane & 15);
+      return *reinterpret_cast<const u32x4*>(rowp + 16 * t * 256 + blk * 16);
+    };
+    u32x4 xb[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) xb[i] = frag(i);
     bf16x8 wf[kPRGW];
 #pragma unroll
-    for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
+    for (int i = 0; i < NS; ++i) {
+      if (i % NT == 0) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const u32x4 xv =
-          *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
+        for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][i / NT], sc[r]);
+      }
+      const u32x4 x = xb[i % PD];
+      if (i + PD < NS) xb[i % PD] = frag(i + PD);
 #pragma unroll
-      for (int r = 0; r < kPRGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
+      for (int r = 0; r < kPRGW; ++r) acc[r][i % NT] = mfma16(wf[r], as_bf16x8(x), acc[r][i % NT]);
     }
+    // The compiler's scheduler would pull the reads back next to their MFMAs; these groups
+    // keep the order: PD reads, then per step four MFMAs and the read PD steps ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
+#pragma unroll
+    for (int i = 0; i < NS - PD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, kPRGW, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < PD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, kPRGW, 0);
   }
 }
 
@@ -263,23 +315,25 @@ constexpr int kPLoadsB = kPRGW + kPRGW / 4;
 constexpr int kPWaitFirst = (kPLead - 1) * kPDma;
 constexpr int kPWait = (kPLead - 1) * kPDma + kPLoadsB;
 constexpr int kPWaitB = 2 * kPDma + kPLoadsB;
-template <int S, int NT, bool ACTIVE, bool FIRST, typename Stage>
+template <int S, int NT, bool ACTIVE, bool FIRST, int PD, typename Stage>
 __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
                                              const PrefillTile& p, int c,
                                              f32x4 (&acc)[kPRGW][NT]) {
+  uint32_t ro[kPDma];
+  prefill_rowoffs<PD>(p, ro);
   prefill_barrier<(FIRST || !ACTIVE) ? kPWaitFirst : kPWait>();
-  prefill_dma(stage(StageC<(S + kPLead) % kPStages>()), p, min(c + kPLead, p.nc - 1));
+  prefill_dma(stage(StageC<(S + kPLead) % kPStages>()), p, min(c + kPLead, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
     prefill_wait_b<kPWaitB>(f[S % 2]);
-    prefill_compute<NT>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc);
+    prefill_compute<NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
     prefill_load_b(f[S % 2], p, min(c + 2, p.nc - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-template <int NT, bool ACTIVE, typename Stage>
+template <int NT, bool ACTIVE, int PD, typename Stage>
 __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTile& p,
                                              f32x4 (&acc)[kPRGW][NT]) {
   PrefillB f[2];
@@ -288,23 +342,25 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
     prefill_load_b(f[1], p, min(1, p.nc - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
-  prefill_dma(stage(StageC<0>()), p, 0);
-  if constexpr (kPLead > 1) prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1));
-  if constexpr (kPLead > 2) prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1));
+  uint32_t ro[kPDma];
+  prefill_rowoffs<PD>(p, ro);
+  prefill_dma(stage(StageC<0>()), p, 0, ro);
+  if constexpr (kPLead > 1) prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1), ro);
+  if constexpr (kPLead > 2) prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
-  prefill_step<0, NT, ACTIVE, true>(stage, f, p, 0, acc);
+  prefill_step<0, NT, ACTIVE, true, PD>(stage, f, p, 0, acc);
   int c = 1;
   for (; c + 4 <= p.nc; c += 4) {
-    prefill_step<1, NT, ACTIVE, false>(stage, f, p, c, acc);
-    prefill_step<2, NT, ACTIVE, false>(stage, f, p, c + 1, acc);
-    prefill_step<3, NT, ACTIVE, false>(stage, f, p, c + 2, acc);
-    prefill_step<0, NT, ACTIVE, false>(stage, f, p, c + 3, acc);
+    prefill_step<1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
+    prefill_step<2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
+    prefill_step<3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
+    prefill_step<0, NT, ACTIVE, false, PD>(stage, f, p, c + 3, acc);
   }
   if (c < p.nc) {
-    prefill_step<1, NT, ACTIVE, false>(stage, f, p, c, acc);
+    prefill_step<1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
     if (c + 1 < p.nc) {
-      prefill_step<2, NT, ACTIVE, false>(stage, f, p, c + 1, acc);
-      if (c + 2 < p.nc) prefill_step<3, NT, ACTIVE, false>(stage, f, p, c + 2, acc);
+      prefill_step<2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
+      if (c + 2 < p.nc) prefill_step<3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
     }
   }
   // The loads issued past the last chunk (clamped re-loads) land before the wave goes
@@ -326,11 +382,22 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
 // ring of kLSlots register chunks (their accumulators leave the registers free), kLSlots
 // chunks ahead.  Wave w brings rows 4 (w + 4j) .. 4 (w + 4j) + 3, j < NT.
 constexpr int kLLead = 7, kLStages = 8, kLSlots = 4;
+#ifndef PFRAG_GU8
+#define PFRAG_GU8 0
+#endif
+constexpr int kPFragGateUp8 = PFRAG_GU8;
 static_assert(kLStages > kLLead && (kLStages & (kLStages - 1)) == 0, "light ring");
 
 template <int NT>
+__device__ __forceinline__ void prefill_rowoffs_light(const PrefillTile& p, uint32_t (&ro)[NT]) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) ro[j] = p.rowoff[4 * (wave + 4 * j) + (lane >> 4)];
+}
+
+template <int NT>
 __device__ __forceinline__ void prefill_dma_light(uint8_t* ring, int slot, const PrefillTile& p,
-                                                  int c) {
+                                                  int c, const uint32_t (&ro)[NT]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   uint8_t* sa = ring + slot * (16 * NT * 256);
 #pragma unroll
@@ -338,7 +405,7 @@ __device__ __forceinline__ void prefill_dma_light(uint8_t* ring, int slot, const
     const int r4 = 4 * (wave + 4 * j);
     const int swz = (lane & 15) ^ ((r4 + (lane >> 4)) & 15);
     const int kcol = c * 128 + swz * 8;
-    const uint32_t off = p.a_off[j] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
+    const uint32_t off = ro[j] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
     uint8_t* dst = sa + r4 * 256;
     const uint32_t lds = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
@@ -361,12 +428,14 @@ template <int SB, int NT, bool ACTIVE, int BAR>
 __device__ __forceinline__ void prefill_step_light(uint8_t* ring, PrefillB (&f)[kLSlots],
                                                    const PrefillTile& p, int c,
                                                    f32x4 (&acc)[kPRGW][NT]) {
+  uint32_t ro[NT];
+  prefill_rowoffs_light<NT>(p, ro);
   prefill_barrier<BAR>();
-  prefill_dma_light<NT>(ring, (c + kLLead) & (kLStages - 1), p, min(c + kLLead, p.nc - 1));
+  prefill_dma_light<NT>(ring, (c + kLLead) & (kLStages - 1), p, min(c + kLLead, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
     prefill_wait_b<kLSlots * NT + (kLSlots - 1) * kPLoadsB>(f[SB]);
-    prefill_compute<NT>(ring + (c & (kLStages - 1)) * (16 * NT * 256), f[SB], p, c, acc);
+    prefill_compute<NT, NT>(ring + (c & (kLStages - 1)) * (16 * NT * 256), f[SB], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
     prefill_load_b(f[SB], p, min(c + kLSlots, p.nc - 1));
     __builtin_amdgcn_sched_barrier(0);
@@ -385,8 +454,10 @@ __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillT
     for (int s = 0; s < kLSlots; ++s) prefill_load_b(f[s], p, min(s, p.nc - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
+  uint32_t ro[NT];
+  prefill_rowoffs_light<NT>(p, ro);
 #pragma unroll
-  for (int v = 0; v < kLLead; ++v) prefill_dma_light<NT>(ring, v, p, min(v, p.nc - 1));
+  for (int v = 0; v < kLLead; ++v) prefill_dma_light<NT>(ring, v, p, min(v, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
   // Steps 0 .. kLLead - 1 have their own barrier counts; nested, so that every path issues
   // the loads in the order the counts assume.
@@ -485,7 +556,7 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
   if constexpr (LIGHT)
     prefill_loop_light<NT, true>(ring, p, acc);
   else
-    prefill_loop<NT, true>(stage, p, acc);
+    prefill_loop<NT, true, GATE_UP && NT == 8 ? kPFragGateUp8 : (NT < 4 ? NT : 4)>(stage, p, acc);
 
   const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
@@ -555,6 +626,7 @@ __global__ void __launch_bounds__(kPThreads)
   constexpr int kS23 = kPStages == 4 ? kPM * 256 : 16;  // stages 2 and 3 exist with 4 stages
   __shared__ __attribute__((aligned(1024))) uint8_t sa01[2][kPM * 256], sa2[kS23], sa3[kS23];
   __shared__ int32_t stok[kPM];
+  __shared__ uint32_t s_rowoff[kPM];
   __shared__ int s_lastw[kPM / 64];  // per wave of slots: last slot holding a real token, or -1
   auto stage = [&](auto s_c) -> uint8_t* {
     constexpr int S = decltype(s_c)::value;
@@ -587,6 +659,12 @@ __global__ void __launch_bounds__(kPThreads)
     int tk = args.tp2id ? args.tp2id[m0 + tid] : (m0 + tid < args.T ? m0 + tid : -1);
     if (tk < 0 || tk >= args.T) tk = -1;
     stok[tid] = tk;
+    // Byte offset of the row's activations.  Padding slots read a real row (token 0 / the
+    // tile's first slot): an MFMA output column depends on its own slot only, and padding
+    // columns are never stored.
+    const uint32_t arow =
+        GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + tid : m0);
+    s_rowoff[tid] = arow * (uint32_t)args.K * 2u;
     const unsigned long long real = __ballot(tk >= 0);
     if (lane == 0) s_lastw[wave] = real ? 64 * wave + 63 - __builtin_clzll(real) : -1;
   }
@@ -609,20 +687,9 @@ __global__ void __launch_bounds__(kPThreads)
   p.nfull = p.K / 128;
   p.tail_q = (p.K % 128) / 32;
   p.a = reinterpret_cast<const char*>(args.a);
-  // Byte offset of tile row `row`'s activations.  Padding slots read a real row (token 0 /
-  // the tile's first slot): an MFMA output column depends on its own slot only, and
-  // padding columns are never stored.
-  auto a_row_off = [&](int row) {
-    const int tk = stok[row];
-    const uint32_t arow =
-        GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + row : m0);
-    return arow * (uint32_t)p.K * 2u;
-  };
+  p.rowoff = s_rowoff;
   const int ntiles = last / 16 + 1;  // real slots of a block come first
   if (ntiles <= 2) {
-    // The light loop's direct loads: rows 4 (wave + 4j) + lane / 16 of the tile.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) p.a_off[j] = a_row_off(4 * (wave + 4 * j) + (lane >> 4));
     uint8_t* ring = &sa01[0][0];
     if (p.rv <= 0) {
       if (ntiles <= 1) {
@@ -641,12 +708,12 @@ __global__ void __launch_bounds__(kPThreads)
     return;
   }
 #pragma unroll
-  for (int i = 0; i < kPDma; ++i) p.a_off[i] = a_row_off((kPM / kPWaves) * wave + 4 * i + (lane >> 4));
+  for (int i = 0; i < kPDma; ++i) p.a_off[i] = s_rowoff[(kPM / kPWaves) * wave + 4 * i + (lane >> 4)];
   if (p.rv <= 0) {
     // No row groups in this tile for this wave: it still brings its share of the
     // activations and meets the barriers.
     f32x4 none[kPRGW][1];
-    prefill_loop<1, false>(stage, p, none);
+    prefill_loop<1, false, 1>(stage, p, none);
     return;
   }
   if (ntiles <= 4)
