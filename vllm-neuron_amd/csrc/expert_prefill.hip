@@ -81,6 +81,14 @@ inline unsigned prefill_grid(int n_mtiles, int n_ntiles, int group) {
 // gives round_bf16's result on every non-NaN input (NaN stays NaN).
 __device__ __forceinline__ float rb(float v) { return (float)(__bf16)v; }
 
+// Two floats -> a packed bf16 pair (a low), by the same conversion: one instruction for
+// both.  A NaN stays a NaN; these are intermediates that later kernels read as numbers.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 __device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
   v = (v > hi) ? hi : v;
   v = (v < lo) ? lo : v;
@@ -526,7 +534,7 @@ __device__ __forceinline__ void gate_up_store(const PrefillArgs& args, const Pre
       const int row = 16 * t + (lane & 15);
       if (stok[row] < 0) continue;
       const f32x4 g4 = acc[2 * pp][t], u4 = acc[2 * pp + 1][t];
-      uint16_t h[4];
+      float h[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float g = rb(g4[i]), u = rb(u4[i]);
@@ -536,10 +544,10 @@ __device__ __forceinline__ void gate_up_store(const PrefillArgs& args, const Pre
         }
         g = clamp_ref(g, args.p.gate_lo, args.p.gate_hi);
         u = clamp_ref(u, args.p.up_lo, args.p.up_hi);
-        h[i] = f32_to_bf16_bits(u * act_bf16<ACT>(g));
+        h[i] = u * act_bf16<ACT>(g);
       }
-      *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * I + col0) =
-          u16x4{h[0], h[1], h[2], h[3]};
+      *reinterpret_cast<u32x2*>(args.out + (size_t)(m0 + row) * I + col0) =
+          u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
     }
   }
 }
@@ -605,15 +613,14 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
       for (int t = 0; t < NT; ++t) {
         const int row = 16 * t + (lane & 15);
         if (stok[row] < 0) continue;
-        uint16_t y[4];
+        float y[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float v = rb(acc[r][t][i]);
-          if (args.bias) v = rb(v + bb[r][i]);
-          y[i] = f32_to_bf16_bits(v);
+          y[i] = acc[r][t][i];
+          if (args.bias) y[i] = rb(rb(y[i]) + bb[r][i]);
         }
-        *reinterpret_cast<u16x4*>(args.out + (size_t)(m0 + row) * H + n0) =
-            u16x4{y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<u32x2*>(args.out + (size_t)(m0 + row) * H + n0) =
+            u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
       }
     }
   }
