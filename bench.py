@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=None)
     ap.add_argument("--prefill-tokens", type=int, default=None)
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--zipf", type=float, default=None,
+                    help="routing skew: router bias -s*log(1 + rank) over a random expert order")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time decode with eager launches")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -78,7 +80,7 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": a.numel(), "copies": 3}))
 
 
-def make_layer(E, K, H, I, limit, biases, dev, gen):
+def make_layer(E, K, H, I, limit, biases, dev, gen, zipf=None):
     import torch
 
     import pkgload
@@ -102,7 +104,12 @@ def make_layer(E, K, H, I, limit, biases, dev, gen):
         gub[:, 1] += 1.0  # the loader pre-adds +1 to the up bias (GPT-OSS)
     dnb = rnorm(E, H) if biases else None
     w = MXFP4Experts(gu_q, gu_s, dn_q, dn_s, gub, dnb, E, H, I)
-    return MXFP4MoE(w, rnorm(E, H), None, K, limit)
+    rb = None
+    if zipf:
+        # Zipf-skewed routing: expert of rank r (a random order) gets logit bias -s*log(1 + r)
+        rank = torch.randperm(E, device=dev, generator=gen).float()
+        rb = (-zipf * torch.log1p(rank)).to(torch.bfloat16)
+    return MXFP4MoE(w, rnorm(E, H), rb, K, limit)
 
 
 def bytes_per_expert(H, I, biases):
@@ -197,7 +204,7 @@ def main():
     pT = args.prefill_tokens or pT
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    layers = [make_layer(E, K, H, I, limit, biases, dev, gen) for _ in range(args.layers)]
+    layers = [make_layer(E, K, H, I, limit, biases, dev, gen, args.zipf) for _ in range(args.layers)]
     L = len(layers)
     xs = [torch.randn(dT, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(L)]
     torch.cuda.synchronize()
@@ -350,6 +357,7 @@ def main():
         "config": {"workload": f"{args.workload}-shaped MoE layer decode, {dT} tokens",
                    "experts": E, "top_k": K, "hidden": H, "intermediate": I,
                    "decode_tokens": dT, "prefill_tokens": pT, "layers_rotated": L,
+                   "routing": "uniform" if not args.zipf else f"zipf s={args.zipf}",
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": None if cpu is None else cpu["decode"],

@@ -34,10 +34,10 @@ __device__ __forceinline__ void tkg_route_block(
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_val, int T, int K, int E,
     int scale_mode, int32_t* __restrict__ expert_off, int32_t* __restrict__ active,
     int32_t* __restrict__ n_active, int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot,
-    float* __restrict__ tok_w) {
+    float* __restrict__ tok_w, int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
   __shared__ unsigned long long masks[16][kTkgMaxE];
   __shared__ int off[kTkgMaxE];
-  __shared__ int wsum[16], wact[16];
+  __shared__ int wsum[16], wact[16], wtile[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = lane; e < E; e += 64) masks[wave][e] = 0ull;  // the rows' first E entries
   __syncthreads();
@@ -67,35 +67,44 @@ __device__ __forceinline__ void tkg_route_block(
   int cnt = 0;
   if (tid < E)
     for (int w = 0; w < 16; ++w) cnt += __popcll(masks[w][tid]);
-  int v = cnt, a = cnt > 0 ? 1 : 0;
+  // Token tiles: 16 of an expert's tokens each (the work unit of the one-tile decode
+  // kernels, so that an expert with many tokens is spread over several waves).
+  const int ntl = (cnt + 15) >> 4;
+  int v = cnt, a = cnt > 0 ? 1 : 0, tl = ntl;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int pv = __shfl_up(v, o), pa = __shfl_up(a, o);
+    const int pv = __shfl_up(v, o), pa = __shfl_up(a, o), pt = __shfl_up(tl, o);
     if (lane >= o) {
       v += pv;
       a += pa;
+      tl += pt;
     }
   }
   if (lane == 63) {
     wsum[wave] = v;
     wact[wave] = a;
+    wtile[wave] = tl;
   }
   __syncthreads();
-  int pv = 0, pa = 0;
+  int pv = 0, pa = 0, pt = 0;
   for (int w = 0; w < wave; ++w) {
     pv += wsum[w];
     pa += wact[w];
+    pt += wtile[w];
   }
   v += pv;
   a += pa;
+  tl += pt;
   if (tid < E) {
     off[tid] = v - cnt;
     expert_off[tid] = v - cnt;
     if (cnt > 0) active[a - 1] = tid;
+    for (int j = 0; j < ntl; ++j) tiles[tl - ntl + j] = (tid << 16) | j;
   }
   if (tid == E - 1) {
     expert_off[E] = v;
     *n_active = a;
+    *n_tiles = tl;
   }
   __syncthreads();
   if (tid >= T) return;
@@ -131,9 +140,9 @@ __global__ void __launch_bounds__(1024) tkg_route_kernel(
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_val, int T, int K, int E,
     int scale_mode, int32_t* __restrict__ expert_off, int32_t* __restrict__ active,
     int32_t* __restrict__ n_active, int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot,
-    float* __restrict__ tok_w) {
+    float* __restrict__ tok_w, int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
   tkg_route_block(topk_idx, topk_val, T, K, E, scale_mode, expert_off, active, n_active, slot_tok,
-                  tok_slot, tok_w);
+                  tok_slot, tok_w, tiles, n_tiles);
 }
 
 // Decode front end for small batches: router logits as 16-token x 16-expert MFMA tiles
@@ -196,7 +205,8 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
     const float* __restrict__ part, const uint16_t* __restrict__ bias, float* __restrict__ logits,
     int T, int E, int K, int act, int act_first, int renorm, float renorm_eps, int scale_mode,
     int32_t* __restrict__ expert_off, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
-    int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot, float* __restrict__ tok_w) {
+    int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot, float* __restrict__ tok_w,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
   __shared__ int32_t s_idx[kFrontMaxT * 8];
   __shared__ float s_val[kFrontMaxT * 8];
   const int tid = threadIdx.x, row = tid >> 4, j = tid & 15;
@@ -243,7 +253,7 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
   }
   __syncthreads();
   tkg_route_block(s_idx, s_val, T, K, E, scale_mode, expert_off, active, n_active, slot_tok,
-                  tok_slot, tok_w);
+                  tok_slot, tok_w, tiles, n_tiles);
 }
 
 // The top-k of 16 tokens per workgroup of 256 threads (token t by the 16-lane row t % 16,
@@ -447,6 +457,8 @@ struct TkgArgs {
   const int32_t* active;
   const int32_t* n_active;
   const int32_t* slot_tok;
+  const int32_t* tiles;    // (expert << 16 | tile) of the routed batch, and their count
+  const int32_t* n_tiles;
   uint16_t* out_hi;        // gate_up: h (hi, lo)
   uint16_t* out_lo;
   float* y;                // down: [slots, H]
@@ -474,8 +486,17 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   const int ai = item / ipe, ri = item - ai * ipe;
   g.cb = 0;
   g.ce = nc;
-  // Item metadata is wave-uniform: keep it in scalar registers.
-  const int e = __builtin_amdgcn_readfirstlane(a.active[ai]);
+  // Item metadata is wave-uniform: keep it in scalar registers.  With one token tile per
+  // pass (NT = 1) an item is (token tile, row groups): an expert's 16-token tiles are
+  // separate items; else (active expert, row groups), looping over the expert's tokens.
+  int e, tb_first = 0;
+  if constexpr (NT == 1) {
+    const int tile = __builtin_amdgcn_readfirstlane(a.tiles[ai]);
+    e = tile >> 16;
+    tb_first = (tile & 0xffff) * 16;
+  } else {
+    e = __builtin_amdgcn_readfirstlane(a.active[ai]);
+  }
   const int rg0 = ri * R;
   g.wq = a.wq + ((size_t)e * n_rg + rg0) * (size_t)g.rg_bytes;
   g.ws = a.ws + ((size_t)e * ((n_rg + 3) / 4) + rg0 / 4) * (size_t)(2 * K);
@@ -485,7 +506,8 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe) {
   const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
                            : reinterpret_cast<const char*>(a.h_hi);
   const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
-  for (int tb = 0; tb < ne; tb += 16 * NT) {
+  const int tb_end = NT == 1 ? min(ne, tb_first + 16) : ne;
+  for (int tb = tb_first; tb < tb_end; tb += 16 * NT) {
     uint32_t row_off[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -548,15 +570,16 @@ __host__ __device__ inline int tkg_items_per_expert(int H, int I, bool gate_up, 
   return (n_rg + R - 1) / R;
 }
 
-// Grid dispatch: wave w of workgroup b takes item WPB * b + w; the grid covers every
-// expert, waves past the active experts' items return at once.  One token tile per
+// Grid dispatch: wave w of workgroup b takes item WPB * b + w; the grid covers the most
+// items a batch can have (every expert, or every possible token tile), waves past the
+// batch's items return at once.  One token tile per
 // item keeps three waves per SIMD (168 registers).
 template <int R, int NT, bool GATE_UP, int D, int WPB>
 __global__ void __launch_bounds__(64 * WPB)
     __attribute__((amdgpu_waves_per_eu(NT == 1 ? 3 : 1))) tkg_stream_kernel(TkgArgs a) {
   const int ipe = tkg_items_per_expert(a.H, a.I, GATE_UP, R);
   const int item = blockIdx.x * WPB + (WPB == 1 ? 0 : wave_id());
-  if (item >= (*a.n_active) * ipe) return;
+  if (item >= (NT == 1 ? *a.n_tiles : *a.n_active) * ipe) return;
   tkg_item<R, NT, GATE_UP, D>(a, item, ipe);
 }
 
@@ -583,8 +606,15 @@ __global__ void __launch_bounds__(256) tkg_combine_kernel(const float* __restric
             f32_to_bf16_bits(acc[3])};
 }
 
+// Token tiles of the routed batch: sum over touched experts of ceil(n_e / 16) with
+// sum n_e = T K, at most when every expert is touched: min(E, T K) + (T K - min(E, T K)) / 16.
+inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
+  const int64_t S = T * K, a = E < S ? E : S;
+  return a + (S - a) / 16;
+}
+
 struct TkgWs {
-  int32_t *expert_off, *active, *n_active, *slot_tok, *tok_slot;
+  int32_t *expert_off, *active, *n_active, *slot_tok, *tok_slot, *tiles, *n_tiles;
   float* tok_w;
   uint16_t *h_hi, *h_lo;
   float* y;
@@ -601,6 +631,8 @@ static size_t tkg_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   t.slot_tok = cv.take<int32_t>(S);
   t.tok_slot = cv.take<int32_t>(S);
   t.tok_w = cv.take<float>(S);
+  t.tiles = cv.take<int32_t>(tkg_max_tiles(T, E, K));
+  t.n_tiles = cv.take<int32_t>(1);
   t.h_hi = cv.take<uint16_t>(S * I);
   t.h_lo = cv.take<uint16_t>(S * I);
   t.y = cv.take<float>(S * H);
@@ -654,11 +686,13 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
   a.active = w.active;
   a.n_active = w.n_active;
   a.slot_tok = w.slot_tok;
+  a.tiles = w.tiles;
+  a.n_tiles = w.n_tiles;
   mark_event(ev, 0, s);
   if (!routed)  // else the decode front end has routed the batch into w
     hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
                        top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
-                       w.tok_slot, w.tok_w);
+                       w.tok_slot, w.tok_w, w.tiles, w.n_tiles);
   mark_event(ev, 1, s);
   TkgArgs gu = a, dn = a;
   gu.x = x;
@@ -673,16 +707,21 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
   dn.ws = dn_s;
   dn.bias = dn_bias;
   dn.y = w.y;
-  // One wave per item; the grid covers every expert (the active count is known on the
-  // device only) and the surplus waves return at once.
-  auto grid = [&](bool gate_up, int R, int wpb) {
-    return dim3((unsigned)((E * tkg_items_per_expert((int)H, (int)I, gate_up, R) + wpb - 1) /
+  // One wave per item; the grid covers the most items the batch can have (the active
+  // experts and token tiles are known on the device only); surplus waves return at once.
+  auto grid = [&](bool gate_up, int R, int wpb, int64_t units) {
+    return dim3((unsigned)((units * tkg_items_per_expert((int)H, (int)I, gate_up, R) + wpb - 1) /
                            wpb));
   };
+  const int64_t n_tile_max = tkg_max_tiles(T, E, top_k);
+  // The one-tile kernels need fewer registers than three waves per SIMD allow; unused
+  // dynamic LDS holds them at three (3 workgroups of 4 waves, or 12 one-wave workgroups,
+  // per CU), the occupancy their item sizes and the dispatcher's spreading are set for.
+  constexpr unsigned kLds3x4 = 50 * 1024, kLds12x1 = 13 * 1024;
   if (T <= 16 || T * top_k <= 8 * E) {
     // One 16-token tile per expert.
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>), grid(true, 4, 4), dim3(256), 0, s,
-                       gu);
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>), grid(true, 4, 4, n_tile_max),
+                       dim3(256), kLds3x4, s, gu);
     mark_event(ev, 2, s);
     // down: with enough items (expected active experts E (1 - (1 - k/E)^T) from the batch
     // size), 8 row groups per item with one chunk in flight, three waves per SIMD, one
@@ -692,17 +731,17 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     const double active_est =
         (double)E * (1.0 - pow(1.0 - (double)top_k / (double)E, (double)T));
     if (active_est * (double)tkg_items_per_expert((int)H, (int)I, false, 8) >= 900.0)
-      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 1, 1>), grid(false, 8, 1), dim3(64), 0,
-                         s, dn);
+      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 1, 1>), grid(false, 8, 1, n_tile_max),
+                         dim3(64), kLds12x1, s, dn);
     else
-      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 4>), grid(false, 4, 4), dim3(256), 0,
-                         s, dn);
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 4>), grid(false, 4, 4, n_tile_max),
+                         dim3(256), kLds3x4, s, dn);
   } else {
     // Two token tiles per pass (an expert with more tokens loops over passes).
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2, 4>), grid(true, 4, 4), dim3(256), 0, s,
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, true, 2, 4>), grid(true, 4, 4, E), dim3(256), 0, s,
                        gu);
     mark_event(ev, 2, s);
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, false, 2, 4>), grid(false, 4, 4), dim3(256), 0,
+    hipLaunchKernelGGL((tkg_stream_kernel<4, 2, false, 2, 4>), grid(false, 4, 4, E), dim3(256), 0,
                        s, dn);
   }
   mark_event(ev, 3, s);
@@ -804,7 +843,7 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
     hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b,    \
                        logits, (int)T, (int)E, top_k, router_act, af, rn, renorm_eps,         \
                        scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok, w.tok_slot, \
-                       w.tok_w);                                                              \
+                       w.tok_w, w.tiles, w.n_tiles);                                          \
   else                                                                                       \
     hipLaunchKernelGGL(front_topk_kernel<P>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, s, \
                        d.part, router_b, logits, (int)T, (int)E, top_k, router_act, af, rn,    \
