@@ -28,6 +28,25 @@ def test_decode_gptoss20b(dev, gptoss20, T):
     check_close(got, want, ties, f"decode 20b T={T}")
 
 
+@pytest.mark.parametrize("E,T,zipf", [(32, 64, 1.2), (64, 48, 1.5)])
+def test_decode_skewed_routing_hot_experts(dev, E, T, zipf):
+    """Zipf-skewed routing: the hottest experts hold several 16-token tiles, each tile its
+    own work item of the decode kernels."""
+    from vllm_neuron_amd import synthetic
+
+    ref, layer, _ = build(synthetic.GPT_OSS_20B, 41, dev, E=E, zipf=zipf)
+    x = synthetic.tokens(43, T, ref.H)
+    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
+    got = layer.decode(x.to(dev), logits_out=logits).cpu()
+    aff, ties = routing_from_logits(logits, ref, x)
+    per_expert = (aff != 0).sum(0)
+    print(f"tokens per expert: max {int(per_expert.max())}, experts touched "
+          f"{int((per_expert > 0).sum())}")
+    assert per_expert.max() > 32  # at least three tiles for one expert
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, f"decode skewed E={E} T={T} zipf={zipf}")
+
+
 @pytest.mark.parametrize("T", [16, 64])
 def test_decode_repeated_calls_and_graph_replays(dev, gptoss20, T):
     """Consecutive calls on one cached workspace, and replays of a captured graph with
