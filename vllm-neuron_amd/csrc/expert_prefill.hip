@@ -390,10 +390,6 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
 // ring of kLSlots register chunks (their accumulators leave the registers free), kLSlots
 // chunks ahead.  Wave w brings rows 4 (w + 4j) .. 4 (w + 4j) + 3, j < NT.
 constexpr int kLLead = 7, kLStages = 8, kLSlots = 4;
-#ifndef PFRAG_GU8
-#define PFRAG_GU8 0
-#endif
-constexpr int kPFragGateUp8 = PFRAG_GU8;
 static_assert(kLStages > kLLead && (kLStages & (kLStages - 1)) == 0, "light ring");
 
 template <int NT>
@@ -564,7 +560,9 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
   if constexpr (LIGHT)
     prefill_loop_light<NT, true>(ring, p, acc);
   else
-    prefill_loop<NT, true, GATE_UP && NT == 8 ? kPFragGateUp8 : (NT < 4 ? NT : 4)>(stage, p, acc);
+    // LDS read-ahead distance: 4 steps (NT steps for 1-2 subtiles); the gate_up 8-subtile
+    // loop has no registers left for it and keeps the compiler's schedule (0).
+    prefill_loop<NT, true, GATE_UP && NT == 8 ? 0 : (NT < 4 ? NT : 4)>(stage, p, acc);
 
   const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
