@@ -91,6 +91,47 @@ def test_moe_cte_api_padding_and_skip_token(dev):
     check_close(got[:150], want[:150], None, "moe_cte padding mask")
 
 
+@pytest.mark.parametrize("act", ["GELU", "SiLU"])
+def test_moe_cte_and_tkg_other_activations(dev, act):
+    """The expert MLP's other activations, unclamped: prefill (moe_cte) and decode
+    (moe_tkg) through the reference call pattern against the oracle's flows."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_block_tkg as obt
+    from oracle import moe_cte as oc
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 61, dev, exp=(118, 122))
+    T = 160
+    x = synthetic.tokens(61, T, ref.H)
+    aff, _ = routing_agreement(layer, ref, x, dev)
+    w = layer.w
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), 8, 2, 256)
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, b2e, 256, conditions=cond,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function=act, skip_token=True,
+                     expert_affinities_scaling_mode="POST_SCALE").cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, 8, 2, 256)
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, am_r, gu, ref.down, gb, db, activation_function=act)
+    check_close(got, want, None, f"moe_cte {act}")
+
+    xd, aff_d = x[:12], aff[:12]
+    idx = torch.topk(aff_d, 2, dim=1).indices.to(torch.int32)
+    got = NF.moe_tkg(xd.to(dev), w.gu_q, w.dn_q, aff_d.to(dev), idx.to(dev), is_all_expert=False,
+                     expert_gate_up_bias=w.gu_bias, expert_down_bias=w.dn_bias,
+                     expert_gate_up_weights_scale=w.gu_s, expert_down_weights_scale=w.dn_s,
+                     expert_affinities_scaling_mode="POST_SCALE", activation_fn=act).cpu()
+    gu4 = ref.gate_up.reshape(8, ref.H, 2, ref.I)
+    want = obt.expert_mlp_fp32_routed(xd, aff_d, gu4, ref.down, ref.gu_bias.reshape(8, 2, ref.I),
+                                      ref.dn_bias, hidden_act_fn=act, scale_mode="POST_SCALE",
+                                      out_dtype=torch.bfloat16)
+    check_close(got, want, None, f"moe_tkg {act}")
+
+
 def test_prefill_and_decode_partial_chunks(dev):
     """K below one 128-wide chunk (gate_up, H = 96) and a partial last chunk (down,
     I = 160); 6 row groups of H leave a partial scale quad."""
