@@ -132,6 +132,21 @@ def test_moe_cte_and_tkg_other_activations(dev, act):
     check_close(got, want, None, f"moe_tkg {act}")
 
 
+@pytest.mark.parametrize("T", [1, 3, 17])
+def test_prefill_tiny_batches(dev, T):
+    """Prefill of a handful of tokens: every M-tile a light one (1-2 subtiles), most of the
+    mapping's blocks empty."""
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 71, dev, exp=(118, 122))
+    x = synthetic.tokens(71 + T, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev), output_dtype=torch.float32).cpu()
+    want, _ = ref.prefill(x, aff)
+    check_close(got, want, ties, f"prefill T={T}")
+
+
 def test_prefill_and_decode_partial_chunks(dev):
     """K below one 128-wide chunk (gate_up, H = 96) and a partial last chunk (down,
     I = 160); 6 row groups of H leave a partial scale quad."""
