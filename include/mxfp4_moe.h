@@ -54,6 +54,11 @@ extern "C" {
 #define MXMOE_ROUTER_SOFTMAX 0
 #define MXMOE_ROUTER_SIGMOID 1
 
+/* Element types (dtype arguments). */
+#define MXMOE_DT_F32 0
+#define MXMOE_DT_F16 1
+#define MXMOE_DT_BF16 2
+
 
 /* Library version (major*10000 + minor*100 + patch). */
 int mxmoe_version(void);
@@ -80,33 +85,63 @@ int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, const uint8_t*
                  int64_t N, int64_t K, uint16_t* y, void* stream);
 
 /*
- * Router: logits = x . W^T (+ bias) in fp32, top-k, activation, scatter.
+ * Router: logits = x . W^T (+ bias), top-k, activation, scatter.
  * Replaces: vllm_neuron/functional/moe/router.py:690-796 (_nki_router_impl, the
- * nkilib router_topk call at :773-794) and the router stage of nkilib moe_block_tkg
- * (moe_block_tkg.py:474-512); semantics of the torch flows at router.py:383-565 and
- * moe_block_tkg.py:152-204.
- * x bf16 [T, H]; w bf16 [E, H] (the storage of router_weights[H, E] = W.T);
- * bias bf16 [E] or NULL.  act_before_topk = 0: top-k on logits, then the
- * activation over the k selected values; = 1: activation over all E logits, then
- * top-k.  renorm = 1 divides the k values by (their sum + renorm_eps).
- * Outputs: logits fp32 [T, E] (always written), affinities fp32 [T, E] (zeros except
- * the k selected), topk_idx int32 [T, k] and topk_val fp32 [T, k] (final values, in
- * descending order; equal values pick the lower expert id).
+ * nkilib router_topk call at :773-794); semantics of the torch flows at router.py:383-565,
+ * computed as torch computes them in compute_dtype (router.py:422-426):
+ *   MXMOE_DT_F32   the operands and products exactly as in an fp32 matmul (x bf16; W bf16
+ *                  or fp16, fp16 weights split exactly into two bf16 operands), fp32 logits
+ *                  and activations;
+ *   MXMOE_DT_F16   x and W cast to fp16, fp16 products summed in fp32, the bias cast to fp16
+ *                  and added in fp32, the logit rounded to fp16 once; every activation
+ *                  output, renorm sum and quotient rounded to fp16 (one rounding per op);
+ *   MXMOE_DT_BF16  the same with bf16.
+ * x [T, H] (x_dtype bf16, or fp16 with compute_dtype fp16); w [E, H] (the storage of
+ * router_weights[H, E] = W.T; w_dtype bf16 or fp16); bias [E] (bias_dtype any) or NULL.
+ * act_before_topk = 0: top-k on logits, then the activation over the k selected values;
+ * = 1: activation over all E logits, then top-k.  renorm = 1 divides the k values by
+ * (their sum + renorm_eps).
+ * Outputs: logits fp32 [T, E] (always written; values of compute_dtype), affinities fp32
+ * [T, E] (zeros except the k selected), topk_idx int32 [T, k] and topk_val fp32 [T, k]
+ * (final values, in descending order; equal values pick the lower expert id).
  */
 size_t mxmoe_router_workspace_bytes(int64_t T, int64_t E);
-int mxmoe_router_topk(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64_t T,
-                      int64_t H, int64_t E, int top_k, int act, int act_before_topk, int renorm,
-                      float renorm_eps, float* logits, float* affinities, int32_t* topk_idx,
-                      float* topk_val, void* workspace, size_t workspace_bytes, void* stream);
+int mxmoe_router_topk(const void* x, int x_dtype, const void* w, int w_dtype, const void* bias,
+                      int bias_dtype, int64_t T, int64_t H, int64_t E, int top_k, int act,
+                      int act_before_topk, int renorm, float renorm_eps, int compute_dtype,
+                      float* logits, float* affinities, int32_t* topk_idx, float* topk_val,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Fused RMSNorm for the decode block: x_norm = bf16(gamma * x * rsqrt(mean(x[:h_actual]^2)
- * + eps)), columns >= h_actual set to 0.
- * Replaces the RMSNorm front-end of vllm_neuron/functional/moe/moe_block_tkg.py:134-150
- * (inside nkilib moe_block_tkg, called at :474-512).  x, out bf16 [T, H]; gamma fp32 [H].
+ * RMSNorm of bf16 rows: out = gamma * (x * inv), inv = 1 / sqrt(ss / h_actual + eps), fp32
+ * arithmetic, rounded to out_dtype (MXMOE_DT_BF16 or MXMOE_DT_F16).
+ *   all_cols = 0: ss sums x^2 over the first h_actual columns and columns >= h_actual
+ *                 are written as 0 (vllm_neuron/functional/moe/moe_block_tkg.py:134-150,
+ *                 the RMSNorm front end of nkilib moe_block_tkg called at :474-512);
+ *   all_cols = 1: ss sums x^2 over all H columns and every column is normalized
+ *                 (rmsnorm_router_topk_tkg.py:249-257; router.py:680-687 with h_actual = H).
+ * x [T, H] bf16; gamma fp32 [H]; out [T, H].
  */
 int mxmoe_rmsnorm(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t h_actual,
-                  float eps, uint16_t* out, void* stream);
+                  int all_cols, float eps, int out_dtype, uint16_t* out, void* stream);
+
+/*
+ * Fused RMSNorm + router top-k of the decode front end, quantization NONE.
+ * Replaces: vllm_neuron/functional/moe/rmsnorm_router_topk_tkg.py:33-45 (the nkilib
+ * kernel behind it); semantics of its torch flow at :214-279: the RMSNorm as
+ * mxmoe_rmsnorm with all_cols = 1, rounded to mm_dtype (MXMOE_DT_F16 or MXMOE_DT_BF16)
+ * into norm_out [T, H]; logits = norm . cast(W, mm_dtype) in fp32 + cast(bias, mm_dtype);
+ * top-k on the fp32 logits, the activation over the k selected values (fp32), scattered
+ * into affinities [T, E] bf16 (zeros elsewhere); topk_idx int32 [T, k].
+ * router_w [E, H] (w_dtype bf16 or fp16), router_b [E] (b_dtype any) or NULL.
+ */
+size_t mxmoe_rmsnorm_router_topk_workspace_bytes(int64_t T, int64_t E, int top_k);
+int mxmoe_rmsnorm_router_topk(const uint16_t* x, const float* gamma, int64_t h_actual, float eps,
+                              const void* router_w, int w_dtype, const void* router_b,
+                              int b_dtype, int64_t T, int64_t H, int64_t E, int top_k, int act,
+                              int mm_dtype, uint16_t* norm_out, int32_t* topk_idx,
+                              uint16_t* affinities, void* workspace, size_t workspace_bytes,
+                              void* stream);
 
 /*
  * Blockwise token -> expert mapping, bit-exact with the reference torch flow.
@@ -170,32 +205,36 @@ int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_
                   size_t workspace_bytes, void* const* stage_events, void* stream);
 
 /*
- * Whole decode expert layer in one call: router (as mxmoe_router_topk) on x, then the
- * mxmoe_moe_tkg pipeline on the selected experts.  The counterpart of the router +
- * expert stages of nkilib moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512)
- * for an already-normalized input; semantics of moe_block_tkg.py:152-297.
- * router_w bf16 [E, H], router_b bf16 [E] or NULL; logits_out fp32 [T, E] or NULL.
+ * Whole decode expert layer in one call: router on x, then the mxmoe_moe_tkg pipeline on
+ * the selected experts.  The counterpart of the router + expert stages of nkilib
+ * moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512) for an
+ * already-normalized input; semantics of moe_block_tkg.py:152-297: fp32 router logits
+ * (router_w [E, H] bf16 or fp16 by router_w_dtype, every product exact; router_b [E] of
+ * router_b_dtype or NULL), then the fp32 expert math.
+ * logits_out fp32 [T, E] or NULL; topk_idx_out int32 [T, k] or NULL (the experts the
+ * front end selected per token, descending score, equal scores -> lower id).
  * stage_events: NULL, or 6 hipEvent_t recorded before the router and after the router,
  * routing, gate_up, down and combine kernels.  For T <= 16 one kernel takes the top-k
  * and routes the batch: the events after the router and after routing then both follow
  * it (routing shows no time of its own).
  */
 size_t mxmoe_moe_decode_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k);
-int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
-                     int router_act, int act_before_topk, int renorm, float renorm_eps,
-                     const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
-                     const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
-                     int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act,
-                     const float* clamps, int scale_mode, uint16_t* out, float* logits_out,
+int mxmoe_moe_decode(const uint16_t* x, const void* router_w, int router_w_dtype,
+                     const void* router_b, int router_b_dtype, int router_act,
+                     int act_before_topk, int renorm, float renorm_eps, const uint8_t* gu_q,
+                     const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
+                     const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H,
+                     int64_t I, int64_t E, int top_k, int act, const float* clamps,
+                     int scale_mode, uint16_t* out, float* logits_out, int32_t* topk_idx_out,
                      void* workspace, size_t workspace_bytes, void* const* stage_events,
                      void* stream);
 
 /*
- * The decode MoE block in one call: RMSNorm (as mxmoe_rmsnorm: variance over the first
- * h_actual columns, bf16 result, columns past h_actual zero) into the workspace, then
- * mxmoe_moe_decode on the normalized rows.  Replaces the RMSNorm + router + expert
- * stages of nkilib moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512;
- * semantics of :134-297) for one expert-parallel rank holding every expert.
+ * The decode MoE block in one call: RMSNorm (as mxmoe_rmsnorm with all_cols = 0 and a bf16
+ * result) into the workspace, then mxmoe_moe_decode on the normalized rows.  Replaces the
+ * RMSNorm + router + expert stages of nkilib moe_block_tkg
+ * (vllm_neuron/functional/moe/moe_block_tkg.py:474-512; semantics of :134-297) for one
+ * expert-parallel rank holding every expert.
  * x bf16 [T, H] (not normalized); gamma fp32 [H]; the rest as mxmoe_moe_decode.
  * stage_events: NULL, or 7 hipEvent_t: before the RMSNorm, then the 6 of
  * mxmoe_moe_decode.
@@ -203,13 +242,15 @@ int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w, const uint16_t
 size_t mxmoe_moe_block_decode_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                               int top_k);
 int mxmoe_moe_block_decode(const uint16_t* x, const float* gamma, int64_t h_actual, float eps,
-                           const uint16_t* router_w, const uint16_t* router_b, int router_act,
-                           int act_before_topk, int renorm, float renorm_eps, const uint8_t* gu_q,
-                           const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
-                           const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H,
-                           int64_t I, int64_t E, int top_k, int act, const float* clamps,
-                           int scale_mode, uint16_t* out, float* logits_out, void* workspace,
-                           size_t workspace_bytes, void* const* stage_events, void* stream);
+                           const void* router_w, int router_w_dtype, const void* router_b,
+                           int router_b_dtype, int router_act, int act_before_topk, int renorm,
+                           float renorm_eps, const uint8_t* gu_q, const uint8_t* gu_s,
+                           const uint8_t* dn_q, const uint8_t* dn_s, const uint16_t* gu_bias,
+                           const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
+                           int top_k, int act, const float* clamps, int scale_mode,
+                           uint16_t* out, float* logits_out, int32_t* topk_idx_out,
+                           void* workspace, size_t workspace_bytes, void* const* stage_events,
+                           void* stream);
 
 /*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour

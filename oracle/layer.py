@@ -27,16 +27,57 @@ import torch
 from . import blockwise, moe_block_tkg, moe_cte, mxfp4, router
 
 
+class LazyExperts:
+    """Per-expert dequantized weights made on first use (a few kept): the indexing the
+    routed forms use (``w[e]``, ``w[e, :, 0, :]``) on a layer too large to dequantize at
+    once.  ``kind`` "gate_up" gives [H, 2, I] per expert, "down" [I, H]."""
+
+    def __init__(self, kind, blocks, scales, E, H, I, keep=4):
+        self.kind, self.blocks, self.scales = kind, blocks, scales
+        self.shape = (E, H, 2, I) if kind == "gate_up" else (E, I, H)
+        self.H, self.I, self.keep = H, I, keep
+        self._cache = {}
+
+    def _get(self, e: int) -> torch.Tensor:
+        w = self._cache.get(e)
+        if w is None:
+            if self.kind == "gate_up":
+                w = mxfp4.gate_up_from_checkpoint(self.blocks[e:e + 1], self.scales[e:e + 1])
+                w = w.reshape(self.H, 2, self.I)
+            else:
+                w = mxfp4.down_from_checkpoint(self.blocks[e:e + 1], self.scales[e:e + 1])[0]
+            if len(self._cache) >= self.keep:
+                self._cache.pop(next(iter(self._cache)))
+            self._cache[e] = w
+        return w
+
+    def __getitem__(self, idx):
+        if isinstance(idx, tuple):
+            return self._get(int(idx[0]))[idx[1:]]
+        return self._get(int(idx))
+
+
 class RefLayer:
-    def __init__(self, lt):
-        """``lt``: a LayerTensors-like object with checkpoint-layout CPU tensors."""
+    def __init__(self, lt, lazy: bool = False):
+        """``lt``: a LayerTensors-like object with checkpoint-layout CPU tensors.  lazy:
+        dequantize experts one at a time when a routed form needs them (the dense flows
+        then are unavailable)."""
         self.shape = lt.shape
         self.K = lt.shape.K
         self.limit = lt.shape.swiglu_limit
-        self.gate_up = mxfp4.gate_up_from_checkpoint(lt.gate_up_blocks, lt.gate_up_scales)
-        self.down = mxfp4.down_from_checkpoint(lt.down_blocks, lt.down_scales)
-        self.E, self.H, twoI = self.gate_up.shape
-        self.I = twoI // 2
+        self.lazy = lazy
+        if lazy:
+            E, twoI, Gh, _ = lt.gate_up_blocks.shape
+            H, I = Gh * 32, twoI // 2
+            self.gate_up = None
+            self.down = LazyExperts("down", lt.down_blocks, lt.down_scales, E, H, I)
+            self._gu_lazy = LazyExperts("gate_up", lt.gate_up_blocks, lt.gate_up_scales, E, H, I)
+            self.E, self.H, self.I = E, H, I
+        else:
+            self.gate_up = mxfp4.gate_up_from_checkpoint(lt.gate_up_blocks, lt.gate_up_scales)
+            self.down = mxfp4.down_from_checkpoint(lt.down_blocks, lt.down_scales)
+            self.E, self.H, twoI = self.gate_up.shape
+            self.I = twoI // 2
         self.gu_bias = (None if lt.gate_up_bias is None
                         else mxfp4.gate_up_bias_from_checkpoint(lt.gate_up_bias))
         self.dn_bias = lt.down_bias
@@ -58,8 +99,14 @@ class RefLayer:
                                        self.router_b, "softmax", None, 1e-6, torch.float32)
 
     # ---- prefill
+    def _gu4(self):
+        """gate_up as [E, H, 2, I] (or its lazy per-expert form)."""
+        if self.lazy:
+            return self._gu_lazy
+        return self.gate_up.reshape(self.E, self.H, 2, self.I)
+
     def _cte_args(self):
-        gu = self.gate_up.reshape(self.E, self.H, 2, self.I)
+        gu = self._gu4()
         gb = None if self.gu_bias is None else self.gu_bias.reshape(self.E, 2, self.I)
         db = None if self.dn_bias is None else self.dn_bias.unsqueeze(1)
         return gu, gb, db
@@ -109,7 +156,7 @@ class RefLayer:
         return out.to(x.dtype), aff
 
     def decode_routed(self, x: torch.Tensor, aff: torch.Tensor):
-        gu = self.gate_up.reshape(self.E, self.H, 2, self.I)
+        gu = self._gu4()
         gb = None if self.gu_bias is None else self.gu_bias.reshape(self.E, 2, self.I)
         return moe_block_tkg.expert_mlp_fp32_routed(
             x, aff, gu, self.down, gb, self.dn_bias, hidden_act_fn=self.act,

@@ -39,9 +39,18 @@ def test_argument_errors_are_reported():
     dummy = ctypes.c_void_p(16)
     rc = lib.mxmoe_dequant_bf16(dummy, dummy, dummy, 4, 31, None)
     assert rc == -1 and b"multiple of 32" in lib.mxmoe_last_error()
-    rc = lib.mxmoe_router_topk(dummy, dummy, None, 4, 64, 8, 9, 0, 0, 0, 0.0, dummy, dummy, dummy,
-                               dummy, None, 0, None)
+    rc = lib.mxmoe_router_topk(dummy, 2, dummy, 2, None, 2, 4, 64, 8, 9, 0, 0, 0, 0.0, 0, dummy,
+                               dummy, dummy, dummy, None, 0, None)
     assert rc == -1 and b"top_k" in lib.mxmoe_last_error()
+    # fp32 computation needs bf16 activations (every product exact)
+    rc = lib.mxmoe_router_topk(dummy, 1, dummy, 2, None, 2, 4, 64, 8, 2, 0, 0, 0, 0.0, 0, dummy,
+                               dummy, dummy, dummy, None, 0, None)
+    assert rc == -1 and b"bf16 activations" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_rmsnorm_router_topk(dummy, dummy, 64, 1e-6, dummy, 1, None, 1, 4, 64, 8, 2, 0,
+                                       0, dummy, dummy, dummy, dummy, 1 << 20, None)
+    assert rc == -1 and b"matmul dtype" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_rmsnorm(dummy, dummy, 4, 64, 65, 0, 1e-6, 2, dummy, None)
+    assert rc == -1 and b"bad shape" in lib.mxmoe_last_error()
     rc = lib.mxmoe_blockwise_mapping(dummy, None, 100, 8, 2, 64, 3, dummy, dummy, dummy, dummy,
                                      None, dummy, 1 << 20, None)
     assert rc == -1 and b"n_blocks" in lib.mxmoe_last_error()
@@ -74,3 +83,82 @@ def test_functional_api_refuses_cpu_tensors():
         NF.router(x, w, 2)
     with pytest.raises(ValueError):
         NF.router(x, w, 9)
+
+
+def test_packed_bias_shapes_are_strict():
+    """Biases of packed experts take [E, 2, I] / [E, 2I] and [E, H] / [E, 1, H] only; the
+    reference's 5-D kernel-layout bias view (model_mxfp4.py:1195-1201) raises instead of
+    being reinterpreted."""
+    import torch
+
+    from vllm_neuron_amd.functional.moe._common import down_bias, gate_up_bias
+
+    E, I, H = 4, 3072, 3072
+    assert gate_up_bias(torch.zeros(E, 2 * I, dtype=torch.bfloat16), E, I).shape == (E, 2, I)
+    assert gate_up_bias(torch.zeros(E, 2, I, dtype=torch.bfloat16), E, I).shape == (E, 2, I)
+    with pytest.raises(ValueError):
+        gate_up_bias(torch.zeros(E, 2 * I, dtype=torch.bfloat16).view(E, 128, 2, 6, 4), E, I)
+    with pytest.raises(ValueError):
+        gate_up_bias(torch.zeros(E, I, 2, dtype=torch.bfloat16), E, I)
+    assert down_bias(torch.zeros(E, 1, H, dtype=torch.bfloat16), E, H).shape == (E, H)
+    with pytest.raises(ValueError):
+        down_bias(torch.zeros(E * H, dtype=torch.bfloat16), E, H)
+
+
+def test_derived_cache_never_aliases_freed_storage():
+    """A cached transposed router weight belongs to its source tensor: a new tensor at a
+    reused address, an in-place update and an inference tensor all get fresh results."""
+    import gc
+
+    import torch
+
+    from vllm_neuron_amd.functional.moe import _cache
+
+    _cache.clear()
+    calls = []
+
+    def make(t):
+        calls.append(1)
+        return t.t().contiguous() * 1
+
+    a = torch.randn(8, 6)
+    r1 = _cache.derived("t", (a,), lambda: make(a))
+    assert _cache.derived("t", (a,), lambda: make(a)) is r1 and len(calls) == 1
+    a.add_(1.0)  # in-place update: version bump
+    r2 = _cache.derived("t", (a,), lambda: make(a))
+    assert len(calls) == 2 and torch.equal(r2, a.t())
+    ptr = a.data_ptr()
+    del a, r1, r2
+    gc.collect()
+    hits = 0
+    for _ in range(20):  # the allocator usually hands the same block to the next tensor
+        b = torch.full((8, 6), 3.0)
+        hits += b.data_ptr() == ptr
+        rb = _cache.derived("t", (b,), lambda: make(b))
+        assert torch.equal(rb, b.t())
+        del b, rb
+        gc.collect()
+    print("address reused", hits, "times")
+    with torch.inference_mode():
+        c = torch.randn(8, 6)
+    n = len(calls)
+    _cache.derived("t", (c,), lambda: make(c))
+    _cache.derived("t", (c,), lambda: make(c))
+    assert len(calls) == n + 2  # inference tensors are never cached
+    v = torch.randn(6, 8)
+    assert _cache.transposed_rows(v.t()).data_ptr() == v.data_ptr()  # [E, H] storage: a view
+
+
+def test_moe_cte_no_scale_raises():
+    import torch
+
+    from vllm_neuron_amd import functional as NF
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="NO_SCALE"):
+        NF.moe_cte(x, torch.zeros(8, 1), torch.zeros(2, 8, 512, dtype=torch.uint8),
+                   torch.zeros(2, 4, 256, dtype=torch.uint8), torch.zeros(256, dtype=torch.int32),
+                   torch.zeros(1, dtype=torch.int32), 256,
+                   gate_up_proj_scale=torch.zeros(2, 1, 128, dtype=torch.uint8),
+                   down_proj_scale=torch.zeros(2, 1, 128, dtype=torch.uint8),
+                   expert_affinities_scaling_mode="NO_SCALE")

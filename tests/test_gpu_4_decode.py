@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from moe_helpers import build, check_close, routing_from_logits
+from moe_helpers import build, check_close, check_indices, decode_checked
 
 pytestmark = pytest.mark.gpu
 
@@ -21,9 +21,7 @@ def test_decode_gptoss20b(dev, gptoss20, T):
 
     ref, layer, _ = gptoss20
     x = synthetic.tokens(21, T, ref.H)
-    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, f"decode 20b T={T}")
 
@@ -36,9 +34,7 @@ def test_decode_skewed_routing_hot_experts(dev, E, T, zipf):
 
     ref, layer, _ = build(synthetic.GPT_OSS_20B, 41, dev, E=E, zipf=zipf)
     x = synthetic.tokens(43, T, ref.H)
-    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     per_expert = (aff != 0).sum(0)
     print(f"tokens per expert: max {int(per_expert.max())}, experts touched "
           f"{int((per_expert > 0).sum())}")
@@ -86,9 +82,7 @@ def test_decode_wide_expert_counts(dev, E, k, T):
     shape = synthetic.MoEShape(f"wide{E}", E, k, 256, 256)
     ref, layer, _ = build(shape, 40 + E, dev, exp=(118, 122))
     x = synthetic.tokens(41, T, ref.H)
-    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, f"decode E={E} k={k} T={T}")
 
@@ -101,9 +95,7 @@ def test_decode_large_batch(dev, gptoss20, T):
 
     ref, layer, _ = gptoss20
     x = synthetic.tokens(33, T, ref.H)
-    logits = torch.empty(T, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     rows = torch.arange(0, T, 7)
     want = ref.decode_routed(x[rows], aff[rows])
     check_close(got[rows], want, ties[rows], f"decode 20b T={T} sample")
@@ -114,9 +106,7 @@ def test_decode_unsaturated_weights(dev):
 
     ref, layer, _ = build(synthetic.GPT_OSS_20B, 2, dev, E=16, exp=(116, 120))
     x = synthetic.tokens(22, 40, ref.H)
-    logits = torch.empty(40, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode unsaturated")
 
@@ -138,9 +128,7 @@ def test_decode_plain_swiglu_fine_grained(dev):
 
     ref, layer, _ = build(synthetic.FINE_GRAINED, 4, dev, E=32)
     x = synthetic.tokens(24, 8, ref.H)
-    logits = torch.empty(8, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode plain swiglu")
 
@@ -274,9 +262,7 @@ def test_decode_gptoss120b_t64_sample(dev):
 
     ref, layer, _ = build(synthetic.GPT_OSS_120B, 7, dev)
     x = synthetic.tokens(27, 64, ref.H)
-    logits = torch.empty(64, ref.E, dtype=torch.float32, device=dev)
-    got = layer.decode(x.to(dev), logits_out=logits).cpu()
-    aff, ties = routing_from_logits(logits, ref, x)
+    got, aff, ties = decode_checked(layer, ref, x, dev)
     rows = torch.arange(0, 64, 8)
     want = ref.decode_routed(x[rows], aff[rows])
     check_close(got[rows], want, ties[rows], "decode 120b T=64 sample")

@@ -122,3 +122,13 @@ def test_block_tkg_impl_matches_layer_decode():
                                      False, False)
     want, _ = layer.decode(xn)
     assert torch.equal(out, want)
+
+
+def test_lazy_layer_matches_eager():
+    """The per-expert lazy dequantization gives the routed forms the same weights."""
+    lt, syn = _mini_layer(E=6, K=2, seed=7)
+    eager, lazy = RefLayer(lt), RefLayer(lt, lazy=True)
+    x = syn.tokens(8, 20, eager.H)
+    aff, _ = eager.route(x)
+    assert torch.equal(eager.decode_routed(x, aff), lazy.decode_routed(x, aff))
+    assert torch.equal(eager.prefill_routed(x, aff), lazy.prefill_routed(x, aff))

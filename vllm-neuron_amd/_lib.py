@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libmxmoe.so"
 ACT_SILU, ACT_GELU, ACT_SWISH = 0, 1, 2
 SCALE_POST, SCALE_NO = 0, 1
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -31,9 +32,12 @@ _SIGNATURES = {
     "mxmoe_dequant_bf16": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_linear": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _P]),
     "mxmoe_router_workspace_bytes": (_SZ, [_I64, _I64]),
-    "mxmoe_router_topk": (_I, [_P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _F, _P, _P, _P, _P,
-                               _P, _SZ, _P]),
-    "mxmoe_rmsnorm": (_I, [_P, _P, _I64, _I64, _I64, _F, _P, _P]),
+    "mxmoe_router_topk": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I, _I, _I, _F, _I,
+                               _P, _P, _P, _P, _P, _SZ, _P]),
+    "mxmoe_rmsnorm": (_I, [_P, _P, _I64, _I64, _I64, _I, _F, _I, _P, _P]),
+    "mxmoe_rmsnorm_router_topk_workspace_bytes": (_SZ, [_I64, _I64, _I]),
+    "mxmoe_rmsnorm_router_topk": (_I, [_P, _P, _I64, _F, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I,
+                                       _I, _P, _P, _P, _P, _SZ, _P]),
     "mxmoe_blockwise_workspace_bytes": (_SZ, [_I64, _I64]),
     "mxmoe_blockwise_mapping": (_I, [_P, _P, _I64, _I64, _I, _I64, _I64, _P, _P, _P, _P, _P, _P,
                                      _SZ, _P]),
@@ -44,12 +48,12 @@ _SIGNATURES = {
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
                            _I, _P, _P, _SZ, _P, _P]),
     "mxmoe_moe_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
-    "mxmoe_moe_decode": (_I, [_P, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
-                              _I64, _I, _I, _P, _I, _P, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_decode": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64,
+                              _I64, _I64, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _SZ, _P, _P]),
     "mxmoe_moe_block_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
-    "mxmoe_moe_block_decode": (_I, [_P, _P, _I64, _F, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P,
-                                    _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I, _P, _P, _P, _SZ,
-                                    _P, _P]),
+    "mxmoe_moe_block_decode": (_I, [_P, _P, _I64, _F, _P, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P,
+                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I, _P, _P,
+                                    _P, _P, _SZ, _P, _P]),
     "mxmoe_probe_hw_dequant": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_probe_mfma": (_I, [_P, _P, _P, _P]),
 }
@@ -132,6 +136,18 @@ def event_array(events):
         if not e.cuda_event:  # torch creates the HIP event on its first record
             e.record()
     return (C.c_void_p * len(events))(*[e.cuda_event for e in events])
+
+
+_TORCH_DT = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
+
+
+def dtype_code(dt: torch.dtype, what: str, allowed=(torch.float32, torch.float16,
+                                                    torch.bfloat16)) -> int:
+    """torch dtype -> MXMOE_DT_* code; NotImplementedError for any other dtype."""
+    if dt not in allowed:
+        names = ", ".join(str(a).replace("torch.", "") for a in allowed)
+        raise NotImplementedError(f"{what} must be one of {names}, got {dt}")
+    return _TORCH_DT[dt]
 
 
 def clamps_array(gate_lo, gate_hi, up_lo, up_hi):

@@ -29,15 +29,34 @@ inline void mark_event(void* const* ev, int i, hipStream_t s) {
   if (ev) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
 }
 
-// Router logits + top-k + activation (router.hip); affinities may be null.
-int router_run(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int64_t T, int64_t H,
-               int64_t E, int top_k, int act, int act_before_topk, int renorm, float renorm_eps,
-               float* logits, float* affinities, int32_t* topk_idx, float* topk_val,
+// Operands and roundings of one router call (router.hip).  Dtypes are MXMOE_DT_* codes;
+// op is how the 16-bit operands are multiplied (kOpBF16, kOpF16 or kOpExact, common.h);
+// the bias, the logits and the activation outputs are rounded to bias_rnd, logit_rnd and
+// act_rnd (MXMOE_DT_F32 leaves them in fp32).
+struct RouterSpec {
+  const uint16_t* x = nullptr;  // [T, H]
+  int x_dt = MXMOE_DT_BF16;
+  const uint16_t* w = nullptr;  // [E, H]
+  int w_dt = MXMOE_DT_BF16;
+  const void* bias = nullptr;  // [E] or null
+  int bias_dt = MXMOE_DT_BF16;
+  int op = 0;
+  int bias_rnd = MXMOE_DT_F32, logit_rnd = MXMOE_DT_F32, act_rnd = MXMOE_DT_F32;
+};
+
+int router_check(const RouterSpec& r);
+
+// Router logits + top-k + activation (router.hip); affinities / aff16 may be null.
+int router_run(const RouterSpec& r, int64_t T, int64_t H, int64_t E, int top_k, int act,
+               int act_before_topk, int renorm, float renorm_eps, float* logits,
+               float* affinities, uint16_t* aff16, int32_t* topk_idx, float* topk_val,
                hipStream_t s);
 
-// RMSNorm over the first ha columns of each row, bf16 out (router.hip).
+// RMSNorm of bf16 rows into bf16 or fp16 (router.hip): the mean square over the first ha
+// columns (all_cols = 0; columns >= ha written as 0) or over all H columns divided by ha
+// (all_cols = 1).
 int rmsnorm_run(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t ha,
-                float eps, uint16_t* out, hipStream_t s);
+                int all_cols, float eps, int out_dt, uint16_t* out, hipStream_t s);
 
 // Bump allocator over a caller-provided workspace.
 struct Carver {

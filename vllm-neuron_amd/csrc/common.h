@@ -62,6 +62,74 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// Round-to-nearest-even float -> fp16 bits (overflow to +-inf, as a tensor cast does).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element types of the C-ABI (MXMOE_DT_*): 0 fp32, 1 fp16, 2 bf16.
+enum Dt : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// How the router multiplies its 16-bit operands (router_logits_kernel).
+constexpr int kOpBF16 = 0, kOpF16 = 1, kOpExact = 2;
+
+// f rounded to the precision of dt (a cast to dt and back to fp32).
+__device__ __forceinline__ float round_to(float f, int dt) {
+  if (dt == kF16) return (float)(_Float16)f;
+  if (dt == kBF16) return round_bf16(f);
+  return f;
+}
+
+// Element i of an array of element type dt, as fp32 (exact).
+__device__ __forceinline__ float load_as_f32(const void* p, size_t i, int dt) {
+  if (dt == kF32) return static_cast<const float*>(p)[i];
+  const uint16_t b = static_cast<const uint16_t*>(p)[i];
+  return dt == kF16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+}
+
+// Eight 16-bit values (a 16-byte load) in one type, as eight of another.
+__device__ __forceinline__ bf16x8 f16x8_to_bf16x8(u32x4 v) {  // RNE, like a tensor cast
+  const u16x8 h = __builtin_bit_cast(u16x8, v);
+  u16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(f16_bits_to_f32(h[i]));
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ f16x8 bf16x8_to_f16x8(u32x4 v) {  // RNE, like a tensor cast
+  const u16x8 h = __builtin_bit_cast(u16x8, v);
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (_Float16)bf16_bits_to_f32(h[i]);
+  return r;
+}
+
+// fp16 values as an exact sum hi + lo of two bf16 values: hi is the value rounded to
+// bf16 (8 significant bits), lo the remainder (at most 3 more bits, also exact), so
+// products with bf16 operands stay exact in fp32 over two bf16 MFMAs.
+__device__ __forceinline__ void f16x8_split_bf16(u32x4 v, bf16x8& hi, bf16x8& lo) {
+  const u16x8 h = __builtin_bit_cast(u16x8, v);
+  u16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float f = f16_bits_to_f32(h[i]);
+    a[i] = f32_to_bf16_bits(f);
+    b[i] = f32_to_bf16_bits(f - bf16_bits_to_f32(a[i]));
+  }
+  hi = __builtin_bit_cast(bf16x8, a);
+  lo = __builtin_bit_cast(bf16x8, b);
+}
+
+__device__ __forceinline__ f32x4 mfma16_f16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // E8M0 exponent byte -> float 2^(s-127); s = 0 gives the subnormal 2^-127 and
 // s = 255 gives +inf (the value 2^128 overflows float).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {

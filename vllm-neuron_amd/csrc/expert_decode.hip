@@ -157,6 +157,9 @@ constexpr int kFrontWaves = 16 / kFrontSlices;  // waves per workgroup
 // Wave w of slice s (blockIdx.z) takes the 128-wide K chunks gw, gw + 16, ... with
 // gw = s * kFrontWaves + w; the workgroup adds its waves' sums in wave order and
 // stores partial s [kFrontSlices, T, E].  A = router rows (experts), B = tokens.
+// WSPLIT: the router weights are fp16, each split exactly into bf16 hi + lo (two MFMAs),
+// so the products are those of the fp32 matmul of the reference flow.
+template <bool WSPLIT>
 __global__ void __launch_bounds__(64 * kFrontWaves) front_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, float* __restrict__ part,
     int T, int H, int E) {
@@ -182,7 +185,14 @@ __global__ void __launch_bounds__(64 * kFrontWaves) front_logits_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       xv[j] = ok ? xv[j] : zero4;
-      acc = mfma16(as_bf16x8(wv[j]), as_bf16x8(xv[j]), acc);
+      if constexpr (WSPLIT) {
+        bf16x8 hi, lo;
+        f16x8_split_bf16(wv[j], hi, lo);
+        acc = mfma16(hi, as_bf16x8(xv[j]), acc);
+        acc = mfma16(lo, as_bf16x8(xv[j]), acc);
+      } else {
+        acc = mfma16(as_bf16x8(wv[j]), as_bf16x8(xv[j]), acc);
+      }
     }
   }
   red[wave][lane] = acc;
@@ -202,21 +212,20 @@ __global__ void __launch_bounds__(64 * kFrontWaves) front_logits_kernel(
 // j, j+16, ...), then the routing of the batch from the selections kept in LDS.
 template <int PER>
 __global__ void __launch_bounds__(1024) front_route_kernel(
-    const float* __restrict__ part, const uint16_t* __restrict__ bias, float* __restrict__ logits,
-    int T, int E, int K, int act, int act_first, int renorm, float renorm_eps, int scale_mode,
+    const float* __restrict__ part, const void* __restrict__ bias, int bias_dt,
+    float* __restrict__ logits, int T, int E, int K, int act, int act_first, int renorm,
+    float renorm_eps, int scale_mode, int32_t* __restrict__ topk_idx_out,
     int32_t* __restrict__ expert_off, int32_t* __restrict__ active, int32_t* __restrict__ n_active,
     int32_t* __restrict__ slot_tok, int32_t* __restrict__ tok_slot, float* __restrict__ tok_w,
     int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
   __shared__ int32_t s_idx[kFrontMaxT * 8];
   __shared__ float s_val[kFrontMaxT * 8];
   const int tid = threadIdx.x, row = tid >> 4, j = tid & 15;
-  // Every load of a token is issued before any is used (addresses clamped into the row,
-  // the bias read from a valid address also when there is none), so the partial sums
-  // and the bias arrive in one round trip.
-  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(part);
-  uint16_t braw[PER];
+  // Every load of a token is issued before any is used (addresses clamped into the row),
+  // so the partial sums and the bias arrive in one round trip.
+  float bval[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) braw[i] = bsrc[min(j + 16 * i, E - 1)];
+  for (int i = 0; i < PER; ++i) bval[i] = bias ? load_as_f32(bias, min(j + 16 * i, E - 1), bias_dt) : 0.f;
   for (int t = row; t < T; t += 64) {
     float pv[kFrontSlices][PER];
 #pragma unroll
@@ -230,14 +239,14 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
       float a = pv[0][i];
 #pragma unroll
       for (int sl = 1; sl < kFrontSlices; ++sl) a += pv[sl][i];
-      a += bias ? bf16_bits_to_f32(braw[i]) : 0.f;
+      a += bval[i];
       const int e = j + 16 * i;
       if (e < E) logits[(size_t)t * E + e] = a;
       v[i] = e < E ? a : -INFINITY;
     }
     int sel_idx[8];
     float out[8];
-    topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+    topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, kF32, sel_idx, out);
     if (j < K) {
       int si = 0;
       float so = 0.f;
@@ -249,6 +258,7 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
         }
       s_idx[t * K + j] = si;
       s_val[t * K + j] = so;
+      if (topk_idx_out) topk_idx_out[t * K + j] = si;
     }
   }
   __syncthreads();
@@ -261,17 +271,16 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
 // work, the front end's VALU-bound part, then spreads over T / 16 CUs.
 template <int PER>
 __global__ void __launch_bounds__(256) front_topk_kernel(
-    const float* __restrict__ part, const uint16_t* __restrict__ bias, float* __restrict__ logits,
-    int T, int E, int K, int act, int act_first, int renorm, float renorm_eps,
-    int32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
+    const float* __restrict__ part, const void* __restrict__ bias, int bias_dt,
+    float* __restrict__ logits, int T, int E, int K, int act, int act_first, int renorm,
+    float renorm_eps, int32_t* __restrict__ topk_idx, float* __restrict__ topk_val) {
   const int tid = threadIdx.x, j = tid & 15;
   const int t = blockIdx.x * 16 + (tid >> 4);
   if (t >= T) return;  // whole 16-lane rows
-  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(part);
-  uint16_t braw[PER];
+  float bval[PER];
   float pv[kFrontSlices][PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) braw[i] = bsrc[min(j + 16 * i, E - 1)];
+  for (int i = 0; i < PER; ++i) bval[i] = bias ? load_as_f32(bias, min(j + 16 * i, E - 1), bias_dt) : 0.f;
 #pragma unroll
   for (int sl = 0; sl < kFrontSlices; ++sl)
 #pragma unroll
@@ -283,14 +292,14 @@ __global__ void __launch_bounds__(256) front_topk_kernel(
     float a = pv[0][i];
 #pragma unroll
     for (int sl = 1; sl < kFrontSlices; ++sl) a += pv[sl][i];
-    a += bias ? bf16_bits_to_f32(braw[i]) : 0.f;
+    a += bval[i];
     const int e = j + 16 * i;
     if (e < E) logits[(size_t)t * E + e] = a;
     v[i] = e < E ? a : -INFINITY;
   }
   int sel_idx[8];
   float out[8];
-  topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+  topk_row_group<16, PER>(v, E, K, act, act_first, renorm, renorm_eps, kF32, sel_idx, out);
   if (j < K) {
     int si = 0;
     float so = 0.f;
@@ -802,14 +811,15 @@ extern "C" size_t mxmoe_moe_decode_workspace_bytes(int64_t T, int64_t H, int64_t
   return decode_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
 }
 
-extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
-                                const uint16_t* router_b, int router_act, int act_before_topk,
-                                int renorm, float renorm_eps, const uint8_t* gu_q,
-                                const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
-                                const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T,
-                                int64_t H, int64_t I, int64_t E, int top_k, int act,
-                                const float* clamps, int scale_mode, uint16_t* out,
-                                float* logits_out, void* workspace, size_t workspace_bytes,
+extern "C" int mxmoe_moe_decode(const uint16_t* x, const void* router_w, int router_w_dtype,
+                                const void* router_b, int router_b_dtype, int router_act,
+                                int act_before_topk, int renorm, float renorm_eps,
+                                const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                                const uint8_t* dn_s, const uint16_t* gu_bias,
+                                const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I,
+                                int64_t E, int top_k, int act, const float* clamps,
+                                int scale_mode, uint16_t* out, float* logits_out,
+                                int32_t* topk_idx_out, void* workspace, size_t workspace_bytes,
                                 void* const* stage_events, void* stream) {
   clear_error();
   MXMOE_REQUIRE(x && router_w && gu_q && gu_s && dn_q && dn_s && out && workspace,
@@ -827,13 +837,30 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
   MXMOE_REQUIRE(router_act == MXMOE_ROUTER_SOFTMAX || router_act == MXMOE_ROUTER_SIGMOID,
                 "moe_decode: unknown router activation %d", router_act);
   MXMOE_REQUIRE(H % 32 == 0, "moe_decode: H=%lld must be a multiple of 32", (long long)H);
+  // The reference decode flow computes the router in fp32 (moe_block_tkg.py:152-162): fp16
+  // router weights are split exactly into two bf16 operands, bf16 ones are exact as they are.
+  RouterSpec r;
+  r.x = x;
+  r.x_dt = kBF16;
+  r.w = static_cast<const uint16_t*>(router_w);
+  r.w_dt = router_w_dtype;
+  r.bias = router_b;
+  r.bias_dt = router_b_dtype;
+  r.op = router_w_dtype == kF16 ? kOpExact : kOpBF16;
+  rc = router_check(r);
+  if (rc) return rc;
   hipStream_t s = as_stream(stream);
   float* logits = logits_out ? logits_out : d.logits;
+  int32_t* idx = topk_idx_out ? topk_idx_out : d.idx;
   mark_event(stage_events, 0, s);
   if (T <= kFrontMaxT) {
-    hipLaunchKernelGGL(front_logits_kernel,
-                       dim3((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16), kFrontSlices),
-                       dim3(64 * kFrontWaves), 0, s, x, router_w, d.part, (int)T, (int)H, (int)E);
+    const dim3 fg((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16), kFrontSlices);
+    if (router_w_dtype == kF16)
+      hipLaunchKernelGGL(front_logits_kernel<true>, fg, dim3(64 * kFrontWaves), 0, s, x, r.w,
+                         d.part, (int)T, (int)H, (int)E);
+    else
+      hipLaunchKernelGGL(front_logits_kernel<false>, fg, dim3(64 * kFrontWaves), 0, s, x, r.w,
+                         d.part, (int)T, (int)H, (int)E);
     const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
     // One token tile: one workgroup takes the top-k and routes (one launch less).  More
     // tiles: the top-k spreads over a workgroup per tile, then the routing kernel.
@@ -841,13 +868,13 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
 #define MXMOE_FRONT(P)                                                                       \
   if (fused)                                                                                 \
     hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b,    \
-                       logits, (int)T, (int)E, top_k, router_act, af, rn, renorm_eps,         \
-                       scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok, w.tok_slot, \
-                       w.tok_w, w.tiles, w.n_tiles);                                          \
+                       router_b_dtype, logits, (int)T, (int)E, top_k, router_act, af, rn,     \
+                       renorm_eps, scale_mode, topk_idx_out, w.expert_off, w.active,          \
+                       w.n_active, w.slot_tok, w.tok_slot, w.tok_w, w.tiles, w.n_tiles);      \
   else                                                                                       \
     hipLaunchKernelGGL(front_topk_kernel<P>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, s, \
-                       d.part, router_b, logits, (int)T, (int)E, top_k, router_act, af, rn,    \
-                       renorm_eps, d.idx, d.val)
+                       d.part, router_b, router_b_dtype, logits, (int)T, (int)E, top_k,       \
+                       router_act, af, rn, renorm_eps, idx, d.val)
     switch (front_per_lane((int)E)) {
       case 1: MXMOE_FRONT(1); break;
       case 2: MXMOE_FRONT(2); break;
@@ -859,14 +886,14 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const uint16_t* router_w,
 #undef MXMOE_FRONT
     rc = check_launch("moe_decode front end");
     if (rc) return rc;
-    return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
+    return tkg_pipeline(x, idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
                         top_k, act, clamps, scale_mode, out, w,
                         stage_events ? stage_events + 1 : nullptr, s, /*routed=*/fused);
   }
-  rc = router_run(x, router_w, router_b, T, H, E, top_k, router_act, act_before_topk, renorm,
-                  renorm_eps, logits, nullptr, d.idx, d.val, s);
+  rc = router_run(r, T, H, E, top_k, router_act, act_before_topk, renorm, renorm_eps, logits,
+                  nullptr, nullptr, idx, d.val, s);
   if (rc) return rc;
-  return tkg_pipeline(x, d.idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
+  return tkg_pipeline(x, idx, d.val, gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E,
                       top_k, act, clamps, scale_mode, out, w,
                       stage_events ? stage_events + 1 : nullptr, s);
 }
@@ -878,12 +905,13 @@ extern "C" size_t mxmoe_moe_block_decode_workspace_bytes(int64_t T, int64_t H, i
 }
 
 extern "C" int mxmoe_moe_block_decode(
-    const uint16_t* x, const float* gamma, int64_t h_actual, float eps, const uint16_t* router_w,
-    const uint16_t* router_b, int router_act, int act_before_topk, int renorm, float renorm_eps,
-    const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
-    const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
-    int top_k, int act, const float* clamps, int scale_mode, uint16_t* out, float* logits_out,
-    void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream) {
+    const uint16_t* x, const float* gamma, int64_t h_actual, float eps, const void* router_w,
+    int router_w_dtype, const void* router_b, int router_b_dtype, int router_act,
+    int act_before_topk, int renorm, float renorm_eps, const uint8_t* gu_q, const uint8_t* gu_s,
+    const uint8_t* dn_q, const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
+    int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act, const float* clamps,
+    int scale_mode, uint16_t* out, float* logits_out, int32_t* topk_idx_out, void* workspace,
+    size_t workspace_bytes, void* const* stage_events, void* stream) {
   clear_error();
   MXMOE_REQUIRE(x && gamma && workspace, "moe_block_decode: null pointer");
   const size_t need = mxmoe_moe_block_decode_workspace_bytes(T, H, I, E, top_k);
@@ -894,10 +922,11 @@ extern "C" int mxmoe_moe_block_decode(
   uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + dec);
   hipStream_t s = as_stream(stream);
   mark_event(stage_events, 0, s);
-  int rc = rmsnorm_run(x, gamma, T, H, h_actual, eps, xn, s);
+  int rc = rmsnorm_run(x, gamma, T, H, h_actual, /*all_cols=*/0, eps, kBF16, xn, s);
   if (rc) return rc;
-  return mxmoe_moe_decode(xn, router_w, router_b, router_act, act_before_topk, renorm, renorm_eps,
-                          gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E, top_k, act, clamps,
-                          scale_mode, out, logits_out, workspace, dec,
-                          stage_events ? stage_events + 1 : nullptr, stream);
+  return mxmoe_moe_decode(xn, router_w, router_w_dtype, router_b, router_b_dtype, router_act,
+                          act_before_topk, renorm, renorm_eps, gu_q, gu_s, dn_q, dn_s, gu_bias,
+                          dn_bias, T, H, I, E, top_k, act, clamps, scale_mode, out, logits_out,
+                          topk_idx_out, workspace, dec, stage_events ? stage_events + 1 : nullptr,
+                          stream);
 }

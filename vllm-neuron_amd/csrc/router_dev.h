@@ -133,13 +133,16 @@ __device__ __forceinline__ void load_row_wave(const float* __restrict__ row, int
 // semantics: act_first = 0: top-k on the logits (descending, equal values -> lower
 // expert id), then the activation over the k selected values; act_first = 1: the
 // activation over all E logits, then top-k.  renorm divides the k values by (their
-// sum + eps).  Every lane returns the same sel_idx[0..K) and out[0..K).
+// sum + eps).  rnd (a Dt) is the precision of the reference's computation dtype: every
+// activation output, the renorm sum and quotient are rounded to it, as the torch ops of
+// router.py:383-503 round each result of a half-precision tensor op (fp32 arithmetic,
+// one rounding per op).  Every lane returns the same sel_idx[0..K) and out[0..K).
 // topk_row_group<W, PER> does the same for a group of W lanes (W = 64: the wave; W = 16:
 // a row of 16 lanes, lane j of the row holding experts j, j+16, ...).
 template <int W, int PER>
 __device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, int K, int act,
                                                int act_first, int renorm, float renorm_eps,
-                                               int (&sel_idx)[8], float (&out)[8]) {
+                                               int rnd, int (&sel_idx)[8], float (&out)[8]) {
   const int lane = threadIdx.x & (W - 1);
   float score[PER];
 #pragma unroll
@@ -158,11 +161,12 @@ __device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, 
       }
       s = group_sum<W>(s);
 #pragma unroll
-      for (int i = 0; i < PER; ++i) score[i] = lane + W * i < E ? score[i] / s : -INFINITY;
+      for (int i = 0; i < PER; ++i)
+        score[i] = lane + W * i < E ? round_to(score[i] / s, rnd) : -INFINITY;
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i)
-        score[i] = lane + W * i < E ? sigmoid_f32(score[i]) : -INFINITY;
+        score[i] = lane + W * i < E ? round_to(sigmoid_f32(score[i]), rnd) : -INFINITY;
     }
   }
   // k rounds of arg-max over the selection keys (descending score, equal scores ->
@@ -201,11 +205,11 @@ __device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, 
         }
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < K) out[k] = out[k] / s;
+        if (k < K) out[k] = round_to(out[k] / s, rnd);
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < K) out[k] = sigmoid_f32(sel_val[k]);
+        if (k < K) out[k] = round_to(sigmoid_f32(sel_val[k]), rnd);
     }
   }
   if (renorm) {
@@ -213,18 +217,18 @@ __device__ __forceinline__ void topk_row_group(const float (&vals)[PER], int E, 
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (k < K) s += out[k];
-    s = s + renorm_eps;
+    s = round_to(s, rnd) + renorm_eps;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (k < K) out[k] = out[k] / s;
+      if (k < K) out[k] = round_to(out[k] / s, rnd);
   }
 }
 
 template <int PER>
 __device__ __forceinline__ void topk_row_wave(const float (&vals)[PER], int E, int K, int act,
                                               int act_first, int renorm, float renorm_eps,
-                                              int (&sel_idx)[8], float (&out)[8]) {
-  topk_row_group<64, PER>(vals, E, K, act, act_first, renorm, renorm_eps, sel_idx, out);
+                                              int rnd, int (&sel_idx)[8], float (&out)[8]) {
+  topk_row_group<64, PER>(vals, E, K, act, act_first, renorm, renorm_eps, rnd, sel_idx, out);
 }
 
 // Values per lane for E experts: the template argument of topk_row_wave.

@@ -2,14 +2,14 @@
 (vllm_neuron/functional/__init__.py:24-33, __all__ :42-74) for the MoE entries."""
 
 from ..enums import (ActFnType, ExpertAffinityScaleMode, MoECTEImplementation,
-                     RouterActFnType, RouterComputationOrder)
+                     QuantizationType, RouterActFnType, RouterComputationOrder)
 from .moe import (build_blockwise_mapping, moe_block_tkg, moe_cte, moe_tkg, num_blocks, rmsnorm,
-                  router)
+                  rmsnorm_router_topk_tkg, router)
 from .mxfp4 import dequantize_mxfp4_to_bf16, mxfp4_linear
 
 __all__ = [
     "router", "build_blockwise_mapping", "moe_cte", "moe_tkg", "moe_block_tkg", "rmsnorm",
-    "num_blocks", "dequantize_mxfp4_to_bf16", "mxfp4_linear", "ActFnType",
-    "ExpertAffinityScaleMode", "MoECTEImplementation", "RouterActFnType",
-    "RouterComputationOrder",
+    "rmsnorm_router_topk_tkg", "num_blocks", "dequantize_mxfp4_to_bf16", "mxfp4_linear",
+    "ActFnType", "ExpertAffinityScaleMode", "MoECTEImplementation", "QuantizationType",
+    "RouterActFnType", "RouterComputationOrder",
 ]

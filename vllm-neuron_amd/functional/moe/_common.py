@@ -2,13 +2,15 @@
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import NamedTuple, Optional
 
 import torch
 from torch import Tensor
 
 from ... import _lib
 from ...enums import member_name
+from ...neuron_layout import experts_from_neuron_layout
+from ._cache import derived
 
 
 def act_code(act) -> int:
@@ -22,11 +24,11 @@ def act_code(act) -> int:
     raise NotImplementedError(f"activation {name} has no MI355X kernel")
 
 
-def scale_code(mode) -> int:
+def scale_code(mode, allow_no_scale: bool = True) -> int:
     name = member_name(mode)
     if name == "POST_SCALE":
         return _lib.SCALE_POST
-    if name == "NO_SCALE":
+    if name == "NO_SCALE" and allow_no_scale:
         return _lib.SCALE_NO
     raise NotImplementedError(f"expert_affinities_scaling_mode {name} has no MI355X kernel")
 
@@ -53,21 +55,104 @@ def expert_shapes(gu_q: Tensor, gu_s: Tensor, dn_q: Tensor, dn_s: Tensor):
 
 
 def gate_up_bias(b: Optional[Tensor], E: int, I: int) -> Optional[Tensor]:
-    """[E, 2, I] or [E, 2I] ([gate | up]) bias -> contiguous bf16 [E, 2, I]."""
+    """gate/up bias of packed experts: [E, 2, I] (gate, up) or [E, 2I] ([gate | up]) bf16
+    -> contiguous [E, 2, I].  Any other shape raises: the reference's kernel-layout views
+    ([E, I/4/n, 2, n, 4], model_mxfp4.py:1195-1201) belong to Trainium-layout weights."""
     if b is None:
         return None
-    if b.numel() != E * 2 * I:
-        raise ValueError(f"gate_up bias has {b.numel()} elements, expected {E * 2 * I}")
+    if tuple(b.shape) not in ((E, 2, I), (E, 2 * I)):
+        raise ValueError(f"gate_up bias must be [{E}, 2, {I}] or [{E}, {2 * I}] for packed "
+                         f"experts, got {tuple(b.shape)}")
     if b.dtype != torch.bfloat16:
         raise NotImplementedError("gate_up bias must be bfloat16")
     return b.reshape(E, 2, I).contiguous()
 
 
 def down_bias(b: Optional[Tensor], E: int, H: int) -> Optional[Tensor]:
+    """down bias of packed experts: [E, H] or [E, 1, H] bf16 -> contiguous [E, H]."""
     if b is None:
         return None
-    if b.numel() != E * H:
-        raise ValueError(f"down bias has {b.numel()} elements, expected {E * H}")
+    if tuple(b.shape) not in ((E, H), (E, 1, H)):
+        raise ValueError(f"down bias must be [{E}, {H}] or [{E}, 1, {H}] for packed experts, "
+                         f"got {tuple(b.shape)}")
     if b.dtype != torch.bfloat16:
         raise NotImplementedError("down bias must be bfloat16")
     return b.reshape(E, H).contiguous()
+
+
+class Experts(NamedTuple):
+    gu_q: Tensor
+    gu_s: Tensor
+    dn_q: Tensor
+    dn_s: Tensor
+    gu_bias: Optional[Tensor]
+    dn_bias: Optional[Tensor]
+    E: int
+    H: int
+    I: int
+
+
+def is_neuron_layout(gate_up_weight: Tensor) -> bool:
+    """The reference's Trainium kernel layout: fp4 x4 packed in 16-bit words, 5-D."""
+    return gate_up_weight.dtype in (torch.uint16, torch.int16) and gate_up_weight.dim() == 5
+
+
+def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
+    """Weights in the layout of the reference's MXFP4 parameters (model_mxfp4.py:957-1018:
+    gate_up [E, 128, 2, H/512, I] uint16 + scale [E, 16, 2, H/512, I] uint8, down
+    [E, 128, I/512, H] uint16 + scale [E, 16, I/512, H] uint8, gate/up bias [E, 2I] in
+    the tiled order (any view of it, e.g. the 5-D one of :1195-1201), down bias [E, H]
+    with the hidden dim shuffled) -> packed experts at the padded sizes.  The padding
+    the reference's loaders add is all zeros (codes, scales, biases), so the padded rows
+    and columns add exact zeros.  Converted once per tensor version."""
+    for t, n, d in ((gu_w, "gate_up weight", 5), (gu_s, "gate_up scale", 5),
+                    (dn_w, "down weight", 4), (dn_s, "down scale", 4)):
+        if t is None:
+            raise AssertionError(f"{n} must be provided for MXFP4 compute")
+        if t.dim() != d:
+            raise ValueError(f"{n}: expected {d}-D kernel-layout tensor, got {tuple(t.shape)}")
+    E = gu_w.shape[0]
+    H_pad = gu_w.shape[3] * 512
+    I_pad = gu_s.shape[4]
+    exp = {"gate_up weight": (E, 128, 2, H_pad // 512, I_pad),
+           "gate_up scale": (E, 16, 2, H_pad // 512, I_pad),
+           "down scale": (E, dn_s.shape[1], dn_s.shape[2], H_pad)}
+    got = {"gate_up weight": tuple(gu_w.shape), "gate_up scale": tuple(gu_s.shape),
+           "down scale": tuple(dn_s.shape)}
+    for k in exp:
+        if exp[k] != got[k]:
+            raise ValueError(f"kernel-layout shapes disagree: {k} is {got[k]}, expected {exp[k]}")
+    if tuple(dn_w.shape) != (E, dn_s.shape[1] * 8, dn_s.shape[2], H_pad):
+        raise ValueError(f"kernel-layout down weight {tuple(dn_w.shape)} does not match its "
+                         f"scale {tuple(dn_s.shape)}")
+    if gu_s.dtype != torch.uint8 or dn_s.dtype != torch.uint8:
+        raise ValueError("MXFP4 scales must be uint8")
+    if gu_b is not None and gu_b.numel() != E * 2 * I_pad:
+        raise ValueError(f"gate_up bias has {gu_b.numel()} elements, expected {E * 2 * I_pad}")
+    if dn_b is not None and dn_b.numel() != E * H_pad:
+        raise ValueError(f"down bias has {dn_b.numel()} elements, expected {E * H_pad}")
+    for b, n in ((gu_b, "gate_up bias"), (dn_b, "down bias")):
+        if b is not None and b.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{n} must be bfloat16")
+
+    def make():
+        ex = experts_from_neuron_layout(
+            gu_w, gu_s, dn_w, dn_s, H_pad, I_pad,
+            None if gu_b is None else gu_b.reshape(E, 2 * I_pad),
+            None if dn_b is None else dn_b.reshape(E, H_pad))
+        return Experts(ex.gu_q, ex.gu_s, ex.dn_q, ex.dn_s, ex.gu_bias, ex.dn_bias, E, H_pad,
+                       I_pad)
+
+    return derived("neuron_layout", (gu_w, gu_s, dn_w, dn_s, gu_b, dn_b), make)
+
+
+def resolve_experts(gu_w: Tensor, gu_s: Optional[Tensor], dn_w: Tensor, dn_s: Optional[Tensor],
+                    gu_b: Optional[Tensor], dn_b: Optional[Tensor]) -> Experts:
+    """The expert arguments of moe_cte / moe_tkg / moe_block_tkg in either layout: this
+    build's packed MXFP4 (uint8, 3-D; biases [E, 2, I] and [E, H]) or the reference's
+    Trainium kernel layout (converted once per tensor version, see _from_neuron_layout)."""
+    if is_neuron_layout(gu_w):
+        return _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b)
+    E, H, I = expert_shapes(gu_w, gu_s, dn_w, dn_s)
+    return Experts(gu_w, gu_s, dn_w, dn_s, gate_up_bias(gu_b, E, I), down_bias(dn_b, E, H), E,
+                   H, I)

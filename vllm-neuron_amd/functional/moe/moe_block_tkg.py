@@ -24,51 +24,29 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import ActFnType, ExpertAffinityScaleMode, RouterActFnType, member_name
-from ._common import act_code, down_bias, expert_shapes, gate_up_bias, scale_code
+from ._cache import transposed_rows
+from ._common import act_code, resolve_experts, scale_code
 from .moe_tkg import moe_tkg_raw
-from .router import router_topk_raw
+from .router import rms_norm, router_topk_raw
 
 
 def rmsnorm(x: Tensor, gamma: Tensor, eps: float, hidden_actual: Optional[int] = None) -> Tensor:
-    """bf16 [T, H] -> bf16 [T, H] with columns >= hidden_actual zeroed."""
-    dev = _lib.require_cuda(x, gamma)
-    T, H = x.shape
-    ha = H if hidden_actual is None else int(hidden_actual)
-    g = gamma.reshape(-1).to(torch.float32).contiguous()
-    if g.numel() != H:
-        raise ValueError(f"gamma has {g.numel()} elements, expected {H}")
-    out = torch.empty_like(x)
-    rc = _lib.lib().mxmoe_rmsnorm(x.contiguous().data_ptr(), g.data_ptr(), T, H, ha, float(eps),
-                                  out.data_ptr(), _lib.stream_handle(dev))
-    _lib.check(rc, "mxmoe_rmsnorm")
-    return out
+    """The decode block's RMSNorm (moe_block_tkg.py:134-150): bf16 [T, H] -> bf16 [T, H],
+    mean square over the first hidden_actual columns, the other columns zeroed."""
+    return rms_norm(x, gamma, eps, hidden_actual, all_cols=False)
 
 
-# The router weights arrive as [H, E] (the reference's layout); the kernels read [E, H].
-# The transposed copy is kept per (storage, version, shape, strides), so a weight tensor
-# passed at every decode step is transposed once (an in-place update bumps its version).
-_ROUTER_T: "dict" = {}
-_ROUTER_T_MAX = 256
+def _router_dtype_code(t: Tensor, what: str) -> int:
+    return _lib.dtype_code(t.dtype, what, (torch.bfloat16, torch.float16))
 
 
-def _router_eh(router_weights: Tensor) -> Tensor:
-    key = (router_weights.data_ptr(), router_weights._version, tuple(router_weights.shape),
-           tuple(router_weights.stride()), str(router_weights.device))
-    w = _ROUTER_T.get(key)
-    if w is None:
-        if len(_ROUTER_T) >= _ROUTER_T_MAX:
-            _ROUTER_T.clear()
-        w = router_weights.t().contiguous()
-        _ROUTER_T[key] = w
-    return w
-
-
-def _block_decode(x, gamma, eps, hidden_actual, router_weights, bias, act, pre_norm, renorm,
-                  top_k, gu_q, gu_s, dn_q, dn_s, gub, dnb, hidden_act, clamps, scale_mode,
-                  want_logits):
-    """mxmoe_moe_block_decode: x bf16 [T, H] (not normalized), router_weights [H, E]."""
-    dev = _lib.require_cuda(x, gamma, router_weights, gu_q)
-    E, H, I = expert_shapes(gu_q, gu_s, dn_q, dn_s)
+def block_decode_raw(x, gamma, eps, hidden_actual, router_weights, bias, act, pre_norm, renorm,
+                     top_k, ex, hidden_act, clamps, scale_mode, want_logits, want_idx=False):
+    """mxmoe_moe_block_decode: x bf16 [T, H] (not normalized), router_weights [H, E]
+    (bf16 or fp16), bias [E] or None, ex: packed experts holding every expert.
+    Returns (out bf16 [T, H], logits fp32 [T, E] or None, topk_idx int32 [T, k] or None)."""
+    dev = _lib.require_cuda(x, gamma, router_weights, ex.gu_q)
+    E, H, I = ex.E, ex.H, ex.I
     T = x.shape[0]
     ha = H if hidden_actual is None else int(hidden_actual)
     g = gamma.reshape(-1).to(torch.float32).contiguous()
@@ -76,22 +54,26 @@ def _block_decode(x, gamma, eps, hidden_actual, router_weights, bias, act, pre_n
         raise ValueError(f"gamma has {g.numel()} elements, expected {H}")
     if x.shape[1] != H:
         raise ValueError(f"hidden states have {x.shape[1]} columns, the experts {H}")
-    w_eh = _router_eh(router_weights)
+    w_eh = transposed_rows(router_weights)
+    wdt = _router_dtype_code(w_eh, "router_weights")
+    bdt = _lib.DT_BF16
     if bias is not None:
-        bias = bias.contiguous()
+        bias = bias.reshape(-1).contiguous()
+        bdt = _lib.dtype_code(bias.dtype, "router_bias")
     x = x.contiguous()
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     logits = torch.empty(T, E, dtype=torch.float32, device=dev) if want_logits else None
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev) if want_idx else None
     L = _lib.lib()
     ws = _lib.workspace(L.mxmoe_moe_block_decode_workspace_bytes(T, H, I, E, top_k), dev)
     rc = L.mxmoe_moe_block_decode(
-        x.data_ptr(), g.data_ptr(), ha, float(eps), w_eh.data_ptr(), _lib.ptr(bias), act,
-        int(pre_norm), int(renorm), 1e-20, gu_q.data_ptr(), gu_s.data_ptr(), dn_q.data_ptr(),
-        dn_s.data_ptr(), _lib.ptr(gub), _lib.ptr(dnb), T, H, I, E, top_k, hidden_act, clamps,
-        scale_mode, out.data_ptr(), _lib.ptr(logits), ws.data_ptr(), ws.numel(), None,
-        _lib.stream_handle(dev))
+        x.data_ptr(), g.data_ptr(), ha, float(eps), w_eh.data_ptr(), wdt, _lib.ptr(bias), bdt,
+        act, int(pre_norm), int(renorm), 1e-20, ex.gu_q.data_ptr(), ex.gu_s.data_ptr(),
+        ex.dn_q.data_ptr(), ex.dn_s.data_ptr(), _lib.ptr(ex.gu_bias), _lib.ptr(ex.dn_bias), T, H,
+        I, E, top_k, hidden_act, clamps, scale_mode, out.data_ptr(), _lib.ptr(logits),
+        _lib.ptr(idx), ws.data_ptr(), ws.numel(), None, _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_block_decode")
-    return out, logits
+    return out, logits, idx
 
 
 def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
@@ -120,8 +102,14 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
                   hidden_actual: Optional[int] = None, skip_router_logits: bool = False,
                   is_all_expert: bool = False,
                   residual: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
-    """inp bf16 [B, S, H] or [T, H]; gamma [1, H] or [H]; router_weights bf16 [H, E];
-    packed expert weights [E_L, ...].  Returns output [T, H] (+ router_logits [T, E])."""
+    """inp bf16 [B, S, H] or [T, H]; gamma [1, H] or [H]; router_weights [H, E] (bf16 or
+    fp16); router_bias [1, E] or [E]; expert weights packed (uint8) or in the reference's
+    Trainium MX layout (uint16 [E_L, 128, 2, H/512, I], converted once per tensor version).
+    Returns output [T, H] (+ router_logits [T, E] fp32).
+
+    router_mm_dtype is accepted and leaves the arithmetic as the reference's torch flow
+    has it: router logits in fp32 from the bf16 normalized rows and the router weights
+    (moe_block_tkg.py:152-162, fp16 weights exactly as fp32)."""
     if shared_expert_gate_w is not None or shared_expert_down_w is not None or \
             shared_expert_up_w is not None:
         raise NotImplementedError("Shared experts have no MI355X kernel")
@@ -134,8 +122,10 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
         inp = inp.reshape(-1, inp.shape[-1])
     if inp.dtype != torch.bfloat16:
         raise NotImplementedError("inp must be bfloat16")
-    E_L, H, I = expert_shapes(expert_gate_up_weights, expert_gate_up_weights_scale,
-                              expert_down_weights, expert_down_weights_scale)
+    ex = resolve_experts(expert_gate_up_weights, expert_gate_up_weights_scale,
+                         expert_down_weights, expert_down_weights_scale, expert_gate_up_bias,
+                         expert_down_bias)
+    E_L = ex.E
     fn = member_name(router_act_fn)
     if fn == "SOFTMAX":
         act = _lib.ROUTER_SOFTMAX
@@ -143,39 +133,27 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
         act = _lib.ROUTER_SIGMOID
     else:
         raise NotImplementedError(f"Router activation {fn} is not supported")
-    if router_weights.dtype != torch.bfloat16:
-        raise NotImplementedError("router_weights must be bfloat16")
-    if router_bias is not None and router_bias.dtype != torch.bfloat16:
-        raise NotImplementedError("router_bias must be bfloat16")
+    _router_dtype_code(router_weights, "router_weights")
     E_g = router_weights.shape[1]
     bias = None if router_bias is None else router_bias.reshape(-1)
+    if bias is not None and bias.numel() != E_g:
+        raise ValueError(f"router_bias has {bias.numel()} elements, expected {E_g}")
+    clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
+                               up_clamp_lower_limit, up_clamp_upper_limit)
     if E_L == E_g:
         # Every expert on this rank: RMSNorm, router and experts in one library call.
-        out, logits = _block_decode(inp, gamma, eps, hidden_actual, router_weights, bias, act,
-                                    bool(router_pre_norm), bool(norm_topk_prob), top_k,
-                                    expert_gate_up_weights, expert_gate_up_weights_scale,
-                                    expert_down_weights, expert_down_weights_scale,
-                                    gate_up_bias(expert_gate_up_bias, E_L, I),
-                                    down_bias(expert_down_bias, E_L, H), act_code(hidden_act_fn),
-                                    _lib.clamps_array(gate_clamp_lower_limit,
-                                                      gate_clamp_upper_limit,
-                                                      up_clamp_lower_limit,
-                                                      up_clamp_upper_limit),
-                                    scale_code(expert_affinities_scaling_mode),
-                                    not skip_router_logits)
+        out, logits, _ = block_decode_raw(inp, gamma, eps, hidden_actual, router_weights, bias,
+                                          act, bool(router_pre_norm), bool(norm_topk_prob),
+                                          top_k, ex, act_code(hidden_act_fn), clamps,
+                                          scale_code(expert_affinities_scaling_mode),
+                                          not skip_router_logits)
         return out if skip_router_logits else (out, logits)
     xn = rmsnorm(inp, gamma, eps, hidden_actual)
-    w_eh = router_weights.t()
-    _, logits, idx, val = router_topk_raw(xn, w_eh, top_k, bias, act, bool(router_pre_norm),
-                                          bool(norm_topk_prob), 1e-20)
+    _, logits, idx, val = router_topk_raw(xn, transposed_rows(router_weights), top_k, bias, act,
+                                          bool(router_pre_norm), bool(norm_topk_prob), 1e-20)
     if E_L < E_g and rank_id is not None:
         idx = idx - E_L * rank_id.reshape(-1)[0].to(idx.dtype)
-    out = moe_tkg_raw(xn, idx, val, expert_gate_up_weights, expert_gate_up_weights_scale,
-                      expert_down_weights, expert_down_weights_scale,
-                      gate_up_bias(expert_gate_up_bias, E_L, I),
-                      down_bias(expert_down_bias, E_L, H), act_code(hidden_act_fn),
-                      _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
-                                        up_clamp_lower_limit, up_clamp_upper_limit),
+    out = moe_tkg_raw(xn, idx, val, ex, act_code(hidden_act_fn), clamps,
                       scale_code(expert_affinities_scaling_mode))
     if skip_router_logits:
         return out

@@ -8,10 +8,16 @@ the blockwise grouped gate_up GEMM with fused MXFP4 dequant, bias, clamps and
 activation, the down GEMM with bias, and the affinity-weighted combine, with the
 bf16 intermediate roundings of ``_torch_moe_impl``.
 
-Weights are the packed MXFP4 layout of vllm_neuron_amd.weights (the reference's
-own MX layout is Trainium-specific): gate_up_proj_weight uint8 [E, 2I/16, 8H] with
-gate_up_proj_scale [E, 2I/16, H/2]; down_proj_weight [E, H/16, 8I] with
-down_proj_scale [E, H/16, I/2].  Trainium tuning arguments (n_block_per_iter,
+Weights are the packed MXFP4 layout of vllm_neuron_amd.weights: gate_up_proj_weight
+uint8 [E, 2I/16, 8H] with gate_up_proj_scale [E, ceil(2I/64), 2H]; down_proj_weight
+[E, H/16, 8I] with down_proj_scale [E, ceil(H/64), 2I]; biases [E, 2, I] and [E, H].
+The reference's own MX parameters (Trainium layout, model_mxfp4.py:957-1018, with the
+tiled bias views of :1408-1420) are accepted as they are and converted once per tensor
+version.
+
+expert_affinities_scaling_mode: POST_SCALE.  The reference torch flow's NO_SCALE adds
+the outputs of every expert for every token, routed or not (moe_cte.py:576-579), which
+a routed kernel does not compute; it raises NotImplementedError here.  Trainium tuning arguments (n_block_per_iter,
 block_sharding_strategy, n_static_blocks, n_dynamic_blocks, checkpoint_activation,
 skip_weight, ...) are accepted and have no effect; ``conditions`` is not needed
 because empty blocks are detected from token_position_to_id.
@@ -26,7 +32,7 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import MoECTEImplementation, QuantizationType, member_name
-from ._common import act_code, down_bias, expert_shapes, gate_up_bias, scale_code
+from ._common import act_code, resolve_experts, scale_code
 
 
 def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_proj_weight: Tensor,
@@ -60,6 +66,7 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
         raise NotImplementedError("output_dtype must be bfloat16 or float32")
     if member_name(quantization_type) == "STATIC_MX":
         raise NotImplementedError("STATIC_MX (FP8 weights) has no MI355X kernel")
+    mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=False)
     if gate_up_activations_T is not None or down_activations is not None:
         raise NotImplementedError("activation checkpoint buffers are not supported")
     if gate_up_proj_scale is None or down_proj_scale is None:
@@ -67,14 +74,15 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
             "gate_up_proj_scale and down_proj_scale must be provided for MX quantized compute")
     dev = _lib.require_cuda(hidden_states, expert_affinities_masked, gate_up_proj_weight,
                             down_proj_weight, token_position_to_id, block_to_expert)
-    E, H, I = expert_shapes(gate_up_proj_weight, gate_up_proj_scale, down_proj_weight,
-                            down_proj_scale)
+    if (gate_and_up_proj_bias is None) != (down_proj_bias is None):
+        raise ValueError("gate_and_up_proj_bias and down_proj_bias must both be provided or neither")
+    ex = resolve_experts(gate_up_proj_weight, gate_up_proj_scale, down_proj_weight,
+                         down_proj_scale, gate_and_up_proj_bias, down_proj_bias)
+    E, H, I = ex.E, ex.H, ex.I
     if hidden_states.dim() != 2 or hidden_states.shape[1] != H:
         raise ValueError(f"hidden_states must be [T(+1), {H}], got {tuple(hidden_states.shape)}")
     if hidden_states.dtype != torch.bfloat16:
         raise NotImplementedError("hidden_states must be bfloat16")
-    if (gate_and_up_proj_bias is None) != (down_proj_bias is None):
-        raise ValueError("gate_and_up_proj_bias and down_proj_bias must both be provided or neither")
     if block_size % 128 != 0:
         raise ValueError(f"block_size must be a multiple of 128, got {block_size}")
     if token_position_to_id.numel() % block_size != 0:
@@ -89,20 +97,16 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
     aff = expert_affinities_masked.reshape(-1).to(torch.float32).contiguous()
     tp2id = token_position_to_id.reshape(-1).to(torch.int32).contiguous()
     b2e = block_to_expert.reshape(-1).to(torch.int32).contiguous()
-    gub = gate_up_bias(gate_and_up_proj_bias, E, I)
-    dnb = down_bias(down_proj_bias, E, H)
     out = torch.empty(T, H, dtype=output_dtype, device=dev)
     L = _lib.lib()
     ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks), dev)
     clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
                                up_clamp_lower_limit, up_clamp_upper_limit)
-    rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), gate_up_proj_weight.contiguous().data_ptr(),
-                         gate_up_proj_scale.contiguous().data_ptr(),
-                         down_proj_weight.contiguous().data_ptr(),
-                         down_proj_scale.contiguous().data_ptr(), _lib.ptr(gub), _lib.ptr(dnb),
-                         tp2id.data_ptr(), b2e.data_ptr(), n_blocks, block_size, T, H, I, E,
-                         act_code(activation_function), clamps,
-                         scale_code(expert_affinities_scaling_mode),
+    rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), ex.gu_q.contiguous().data_ptr(),
+                         ex.gu_s.contiguous().data_ptr(), ex.dn_q.contiguous().data_ptr(),
+                         ex.dn_s.contiguous().data_ptr(), _lib.ptr(ex.gu_bias),
+                         _lib.ptr(ex.dn_bias), tp2id.data_ptr(), b2e.data_ptr(), n_blocks,
+                         block_size, T, H, I, E, act_code(activation_function), clamps, mode,
                          int(output_dtype == torch.float32), out.data_ptr(), ws.data_ptr(),
                          ws.numel(), _lib.event_array(stage_events), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_cte")

@@ -21,24 +21,27 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import ExpertAffinityScaleMode, MoEAllToAllVStrategy, member_name
-from ._common import act_code, down_bias, expert_shapes, gate_up_bias, scale_code
+from ._common import Experts, act_code, resolve_experts, scale_code
 
 
-def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, gu_q, gu_s, dn_q, dn_s, gub, dnb,
-                act: int, clamps, scale_mode: int, stage_events=None) -> Tensor:
-    """Kernel call: x bf16 [T, H], topk_idx int32 [T, k] (local ids), topk_val fp32 [T, k].
-    stage_events: optional 5 torch.cuda.Event recorded around routing, gate_up, down and
-    combine."""
-    dev = _lib.require_cuda(x, topk_idx, topk_val, gu_q)
-    E, H, I = expert_shapes(gu_q, gu_s, dn_q, dn_s)
+def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, ex: Experts, act: int, clamps,
+                scale_mode: int, stage_events=None) -> Tensor:
+    """Kernel call: x bf16 [T, H], topk_idx int32 [T, k] (local ids), topk_val fp32 [T, k],
+    ex packed experts.  stage_events: optional 5 torch.cuda.Event recorded around routing,
+    gate_up, down and combine."""
+    dev = _lib.require_cuda(x, topk_idx, topk_val, ex.gu_q)
+    E, H, I = ex.E, ex.H, ex.I
+    if x.dim() != 2 or x.shape[1] != H:
+        raise ValueError(f"hidden states must be [T, {H}], got {tuple(x.shape)}")
     T, K = topk_idx.shape
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     L = _lib.lib()
     ws = _lib.workspace(L.mxmoe_moe_tkg_workspace_bytes(T, H, I, E, K), dev)
     rc = L.mxmoe_moe_tkg(x.contiguous().data_ptr(), topk_idx.contiguous().data_ptr(),
-                         topk_val.contiguous().data_ptr(), gu_q.data_ptr(), gu_s.data_ptr(),
-                         dn_q.data_ptr(), dn_s.data_ptr(), _lib.ptr(gub), _lib.ptr(dnb), T, H, I,
-                         E, K, act, clamps, scale_mode, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                         topk_val.contiguous().data_ptr(), ex.gu_q.data_ptr(), ex.gu_s.data_ptr(),
+                         ex.dn_q.data_ptr(), ex.dn_s.data_ptr(), _lib.ptr(ex.gu_bias),
+                         _lib.ptr(ex.dn_bias), T, H, I, E, K, act, clamps, scale_mode,
+                         out.data_ptr(), ws.data_ptr(), ws.numel(),
                          _lib.event_array(stage_events), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_tkg")
     return out
@@ -65,27 +68,28 @@ def moe_tkg(hidden_input: Tensor, expert_gate_up_weights: Tensor, expert_down_we
             input_dequant_scale: Optional[Tensor] = None,
             all_to_all_v_strategy=MoEAllToAllVStrategy.DISABLED) -> Tensor:
     """hidden_input bf16 [T, H]; expert_affinities [T, E] (global ids); expert_index [T, K].
-    Weights packed (see moe_cte).  Returns [T, H] in output_dtype (bf16 by default)."""
+    Weights packed or in the reference's Trainium MX layout (see moe_cte).  Returns [T, H]
+    in output_dtype (bf16 by default)."""
     if member_name(all_to_all_v_strategy) != "DISABLED":
         raise NotImplementedError("all-to-all-v packed inputs need several GPUs")
     if hidden_input_scale is not None or expert_gate_up_input_scale is not None or \
             expert_down_input_scale is not None or input_dequant_scale is not None:
         raise NotImplementedError("FP8 activation quantization has no MI355X kernel")
-    if expert_gate_up_weights.dtype != torch.uint8:
+    if expert_gate_up_weights.dtype not in (torch.uint8, torch.uint16, torch.int16):
         raise NotImplementedError(
-            f"moe_tkg only supports packed MXFP4 weights, got {expert_gate_up_weights.dtype}")
+            f"moe_tkg only supports MXFP4 weights, got {expert_gate_up_weights.dtype}")
     if hidden_input.dtype != torch.bfloat16:
         raise NotImplementedError("hidden_input must be bfloat16")
-    E_L, H, I = expert_shapes(expert_gate_up_weights, expert_gate_up_weights_scale,
-                              expert_down_weights, expert_down_weights_scale)
+    if expert_affinities is None or expert_index is None:
+        raise ValueError("expert_affinities and expert_index are required")
+    ex = resolve_experts(expert_gate_up_weights, expert_gate_up_weights_scale,
+                         expert_down_weights, expert_down_weights_scale, expert_gate_up_bias,
+                         expert_down_bias)
     idx = expert_index.to(torch.int64)
     val = torch.gather(expert_affinities.to(torch.float32), 1, idx)
     if rank_id is not None:
-        idx = idx - E_L * rank_id.reshape(-1)[0].to(idx.dtype)
-    out = moe_tkg_raw(hidden_input, idx.to(torch.int32), val, expert_gate_up_weights,
-                      expert_gate_up_weights_scale, expert_down_weights,
-                      expert_down_weights_scale, gate_up_bias(expert_gate_up_bias, E_L, I),
-                      down_bias(expert_down_bias, E_L, H), act_code(activation_fn),
+        idx = idx - ex.E * rank_id.reshape(-1)[0].to(idx.dtype)
+    out = moe_tkg_raw(hidden_input, idx.to(torch.int32), val, ex, act_code(activation_fn),
                       _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
                                         up_clamp_lower_limit, up_clamp_upper_limit),
                       scale_code(expert_affinities_scaling_mode))

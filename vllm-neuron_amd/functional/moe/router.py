@@ -3,8 +3,12 @@
 Mirrors vllm_neuron/functional/moe/router.py:71-297 (same signature, argument
 meaning, validation and exception types, _validate_router_inputs :601-677).  The
 reference dispatches to nkilib router_topk (:690-796) or its torch flow
-(:383-565); here every supported call runs mxmoe_router_topk and anything the
-kernel does not cover raises NotImplementedError (there is no CPU path).
+(:383-565); here every supported call runs mxmoe_router_topk (after mxmoe_rmsnorm when
+gamma is given) and anything the kernels do not cover raises NotImplementedError
+(there is no CPU path).  computation_dtype float32, float16 and bfloat16 follow the
+torch flow's arithmetic in that dtype (router.py:414-440): operands cast to it, fp32
+sums of the products, one rounding per tensor op; the GPT-OSS MXFP4 model passes
+float16 with float16 router weights (model_mxfp4.py:950-955, :1337-1344).
 
 Computation orders: PRENORM_LINEAR_TOPK_ACT_SCATTER and
 PRENORM_LINEAR_ACT_TOPK_RENORM_SCATTER run as in the reference.
@@ -22,6 +26,7 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import RouterComputationOrder
+from ._cache import transposed_rows
 
 
 def _validate_router_inputs(hidden_states, router_weights, top_k, router_bias, gamma,
@@ -67,13 +72,19 @@ def _act_code(activation) -> int:
 
 
 def router_topk_raw(x: Tensor, w_eh: Tensor, top_k: int, bias: Optional[Tensor], act: int,
-                    act_before_topk: bool, renorm: bool, renorm_eps: float = 0.0):
-    """Kernel call.  x bf16 [T, H]; w_eh bf16 [E, H] contiguous; bias bf16 [E] or None.
-    Returns (affinities fp32 [T, E], logits fp32 [T, E], topk_idx int32 [T, k],
-    topk_val fp32 [T, k])."""
+                    act_before_topk: bool, renorm: bool, renorm_eps: float = 0.0,
+                    compute_dtype: torch.dtype = torch.float32):
+    """Kernel call.  x bf16 (or fp16 with compute_dtype fp16) [T, H]; w_eh bf16/fp16 [E, H];
+    bias [E] (fp32, fp16 or bf16) or None.  Returns (affinities [T, E], logits [T, E],
+    topk_idx int32 [T, k], topk_val fp32 [T, k]); affinities and logits in fp32 holding
+    values of compute_dtype."""
     dev = _lib.require_cuda(x, w_eh, bias)
     T, H = x.shape
     E = w_eh.shape[0]
+    xdt = _lib.dtype_code(x.dtype, "hidden_states", (torch.bfloat16, torch.float16))
+    wdt = _lib.dtype_code(w_eh.dtype, "router_weights", (torch.bfloat16, torch.float16))
+    bdt = _lib.DT_BF16 if bias is None else _lib.dtype_code(bias.dtype, "router_bias")
+    cdt = _lib.dtype_code(compute_dtype, "computation_dtype")
     x = x.contiguous()
     w_eh = w_eh.contiguous()
     if bias is not None:
@@ -83,18 +94,36 @@ def router_topk_raw(x: Tensor, w_eh: Tensor, top_k: int, bias: Optional[Tensor],
     idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
     val = torch.empty(T, top_k, dtype=torch.float32, device=dev)
     L = _lib.lib()
-    rc = L.mxmoe_router_topk(x.data_ptr(), w_eh.data_ptr(), _lib.ptr(bias), T, H, E, top_k, act,
-                             int(act_before_topk), int(renorm), float(renorm_eps),
-                             logits.data_ptr(), aff.data_ptr(), idx.data_ptr(), val.data_ptr(),
-                             None, 0, _lib.stream_handle(dev))
+    rc = L.mxmoe_router_topk(x.data_ptr(), xdt, w_eh.data_ptr(), wdt, _lib.ptr(bias), bdt, T, H,
+                             E, top_k, act, int(act_before_topk), int(renorm), float(renorm_eps),
+                             cdt, logits.data_ptr(), aff.data_ptr(), idx.data_ptr(),
+                             val.data_ptr(), None, 0, _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_router_topk")
     return aff, logits, idx, val
 
 
-def _as_bf16(t: Optional[Tensor], what: str) -> Optional[Tensor]:
-    if t is None or t.dtype == torch.bfloat16:
-        return t
-    raise NotImplementedError(f"{what} must be bfloat16 for the MI355X router kernel, got {t.dtype}")
+def rms_norm(x: Tensor, gamma: Tensor, eps: float, hidden_actual: Optional[int] = None,
+             all_cols: bool = True, out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """mxmoe_rmsnorm: bf16 [T, H] -> [T, H] in out_dtype (bf16 or fp16; default bf16).
+    all_cols: mean square over all H columns divided by hidden_actual (router.py:680-687
+    with hidden_actual = H, rmsnorm_router_topk_tkg.py:249-257); otherwise over the
+    first hidden_actual columns with the others zeroed (moe_block_tkg.py:134-150)."""
+    dev = _lib.require_cuda(x, gamma)
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError(f"the MI355X RMSNorm takes bfloat16 rows, got {x.dtype}")
+    T, H = x.shape
+    ha = H if hidden_actual is None else int(hidden_actual)
+    g = gamma.reshape(-1).to(torch.float32).contiguous()
+    if g.numel() != H:
+        raise ValueError(f"gamma has {g.numel()} elements, expected {H}")
+    odt = torch.bfloat16 if out_dtype is None else out_dtype
+    code = _lib.dtype_code(odt, "RMSNorm output", (torch.bfloat16, torch.float16))
+    out = torch.empty(T, H, dtype=odt, device=dev)
+    rc = _lib.lib().mxmoe_rmsnorm(x.contiguous().data_ptr(), g.data_ptr(), T, H, ha,
+                                  int(all_cols), float(eps), code, out.data_ptr(),
+                                  _lib.stream_handle(dev))
+    _lib.check(rc, "mxmoe_rmsnorm")
+    return out
 
 
 def router(hidden_states: Tensor, router_weights: Tensor, top_k: int,
@@ -109,8 +138,11 @@ def router(hidden_states: Tensor, router_weights: Tensor, top_k: int,
            use_indirect_dma_scatter: Optional[bool] = None,
            use_PE_broadcast_w_bias: Optional[bool] = None) -> Union[Tensor, Tuple[Tensor, Tensor]]:
     """Router API (router.py:71-297).  hidden_states bf16 [T, H] (or [H, T] when
-    transposed), router_weights bf16 [H, E] (typically ``W.T`` of a [E, H] parameter),
-    router_bias bf16 [E].  Returns affinities [T, E] fp32 (+ logits [T, E] fp32).
+    transposed), router_weights bf16/fp16 [H, E] (typically ``W.T`` of a [E, H]
+    parameter), router_bias [E], gamma [H] (optional RMSNorm before the router,
+    router.py:680-687).  Returns affinities [T, E] (+ logits [T, E]) in
+    ``computation_dtype``, computed as the torch flow computes them in that dtype
+    (router.py:414-440).
 
     Kernel-only tuning arguments of the reference (shard_on_tokens, x_sb_layout,
     use_column_tiling, use_indirect_dma_scatter, use_PE_broadcast_w_bias) are accepted
@@ -119,16 +151,18 @@ def router(hidden_states: Tensor, router_weights: Tensor, top_k: int,
                             computation_dtype, router_computation_order,
                             transposed_hidden_states)
     act = _act_code(activation)
-    if gamma is not None:
-        raise NotImplementedError("router(gamma=...) has no MI355X kernel; use moe_block_tkg for "
-                                  "the fused RMSNorm + router")
-    if computation_dtype != torch.float32:
-        raise NotImplementedError("the MI355X router computes in float32 only")
     x = hidden_states.t() if transposed_hidden_states else hidden_states
-    x = _as_bf16(x, "hidden_states")
-    w_eh = _as_bf16(router_weights, "router_weights").t()
-    bias = _as_bf16(router_bias, "router_bias")
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            f"the MI355X router takes bfloat16 hidden_states, got {x.dtype}")
+    if gamma is not None:
+        x = rms_norm(x, gamma, eps)
+    w_eh = transposed_rows(router_weights)
     name = getattr(router_computation_order, "name", "")
     act_first = name == "PRENORM_LINEAR_ACT_TOPK_RENORM_SCATTER"
-    aff, logits, _, _ = router_topk_raw(x, w_eh, top_k, bias, act, act_first, act_first, 0.0)
+    aff, logits, _, _ = router_topk_raw(x, w_eh, top_k, router_bias, act, act_first, act_first,
+                                        0.0, computation_dtype)
+    if computation_dtype != torch.float32:  # the values already are of that dtype
+        aff = aff.to(computation_dtype)
+        logits = logits.to(computation_dtype)
     return (aff, logits) if return_logits else aff

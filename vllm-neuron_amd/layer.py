@@ -32,8 +32,12 @@ class MXFP4MoE:
                  router_b: Optional[torch.Tensor], top_k: int,
                  swiglu_limit: Optional[float] = 7.0, block_size: int = BLOCK_SIZE):
         self.w = experts
-        self.router_w = router_w.contiguous()  # [E, H] bf16
-        self.router_b = router_b
+        self.router_w = router_w.contiguous()  # [E, H] bf16 or fp16
+        self.router_b = None if router_b is None else router_b.contiguous()
+        self._w_dt = _lib.dtype_code(self.router_w.dtype, "router weights",
+                                     (torch.bfloat16, torch.float16))
+        self._b_dt = (_lib.DT_BF16 if router_b is None
+                      else _lib.dtype_code(router_b.dtype, "router bias"))
         self.top_k = top_k
         self.block_size = block_size
         self.limit = swiglu_limit
@@ -70,9 +74,11 @@ class MXFP4MoE:
                        up_clamp_upper_limit=u_hi, up_clamp_lower_limit=u_lo,
                        output_dtype=output_dtype, stage_events=stage_events)
 
-    def decode(self, x: torch.Tensor, stage_events=None, logits_out=None):
+    def decode(self, x: torch.Tensor, stage_events=None, logits_out=None, topk_idx_out=None):
         """Router + experts in one library call (mxmoe_moe_decode).  The workspace is
-        cached per token count, so calls of one layer object belong on one stream."""
+        cached per token count, so calls of one layer object belong on one stream.
+        logits_out fp32 [T, E] / topk_idx_out int32 [T, k]: optional outputs of the
+        front end (the logits and the experts it selected)."""
         w = self.w
         T, H = x.shape
         dev = _lib.require_cuda(x, w.gu_q)
@@ -86,11 +92,11 @@ class MXFP4MoE:
         x = x.contiguous()
         out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
         rc = L.mxmoe_moe_decode(
-            x.data_ptr(), self.router_w.data_ptr(), _lib.ptr(self.router_b), _lib.ROUTER_SOFTMAX,
-            0, 0, 0.0, w.gu_q.data_ptr(), w.gu_s.data_ptr(), w.dn_q.data_ptr(),
-            w.dn_s.data_ptr(), _lib.ptr(w.gu_bias), _lib.ptr(w.dn_bias), T, H, w.I, w.E,
-            self.top_k, self.act, self._clamps, _lib.SCALE_POST, out.data_ptr(),
-            _lib.ptr(logits_out), ws.data_ptr(), ws.numel(), _lib.event_array(stage_events),
-            _lib.stream_handle(dev))
+            x.data_ptr(), self.router_w.data_ptr(), self._w_dt, _lib.ptr(self.router_b),
+            self._b_dt, _lib.ROUTER_SOFTMAX, 0, 0, 0.0, w.gu_q.data_ptr(), w.gu_s.data_ptr(),
+            w.dn_q.data_ptr(), w.dn_s.data_ptr(), _lib.ptr(w.gu_bias), _lib.ptr(w.dn_bias), T, H,
+            w.I, w.E, self.top_k, self.act, self._clamps, _lib.SCALE_POST, out.data_ptr(),
+            _lib.ptr(logits_out), _lib.ptr(topk_idx_out), ws.data_ptr(), ws.numel(),
+            _lib.event_array(stage_events), _lib.stream_handle(dev))
         _lib.check(rc, "mxmoe_moe_decode")
         return out

@@ -10,7 +10,8 @@ those loaders (one tensor-parallel rank, tp_degree = 1) can be handed to
 checkpoint (``MXFP4Experts.from_split``).  The kernels work at the true H and I (no
 padding), so the padded tail is dropped.
 
-Every step is a pure permutation of bytes (torch views, permutes and slices).
+Every step is a pure permutation of bytes (torch views, permutes and slices); the
+16-bit words move as int16, which every torch device can copy.
 """
 
 from __future__ import annotations
@@ -50,7 +51,7 @@ def _inverse(perm):
 
 
 def untile_gate_up_blocks(w: torch.Tensor, H_pad: int, I_pad: int) -> torch.Tensor:
-    """[E, 128, 2, H_pad/512, ...] uint16 -> [E, H_pad/4, 2 I_pad] uint16 (gate | up)."""
+    """[E, 128, 2, H_pad/512, ...] 16-bit words -> [E, H_pad/4, 2 I_pad] (gate | up)."""
     E = w.shape[0]
     nHt, qbH = _h_tiling(H_pad)
     nIt, qbI = _i_tiling(I_pad)
@@ -79,7 +80,7 @@ def untile_gate_up_bias(b: torch.Tensor, I_pad: int) -> torch.Tensor:
 
 
 def untile_down_blocks(w: torch.Tensor, H_pad: int, I_pad: int) -> torch.Tensor:
-    """[E, 128, I_pad/512, H_pad] uint16 -> [E, I_pad/4, H_pad] uint16."""
+    """[E, 128, I_pad/512, H_pad] 16-bit words -> [E, I_pad/4, H_pad]."""
     E = w.shape[0]
     nIt, qbI = _i_tiling(I_pad)
     perm = (0, 2, 3, 1, 5, 4, 6)
@@ -124,7 +125,7 @@ def experts_from_neuron_layout(gate_up_blocks: torch.Tensor, gate_up_scales: tor
     if H > H_pad or I > I_pad or H % 32 or I % 32:
         raise ValueError(f"H={H}, I={I} must be multiples of 32 within the padded {H_pad}, {I_pad}")
     # gate_up: untile, transpose back, bytes [E, 2 I_pad, H_pad/32, 16], split, trim
-    g = untile_gate_up_blocks(gate_up_blocks.view(torch.uint16), H_pad, I_pad)
+    g = untile_gate_up_blocks(gate_up_blocks.view(torch.int16), H_pad, I_pad)
     g = g.transpose(1, 2).contiguous().view(torch.uint8).reshape(E, 2 * I_pad, H_pad // 32, 16)
     gate_b, up_b = g[:, :I], g[:, I_pad:I_pad + I]
     s = untile_gate_up_scale(gate_up_scales, H_pad, I_pad).transpose(1, 2)
@@ -132,7 +133,7 @@ def experts_from_neuron_layout(gate_up_blocks: torch.Tensor, gate_up_scales: tor
     gate_b, up_b = gate_b[:, :, :H // 32], up_b[:, :, :H // 32]
     gate_s, up_s = gate_s[:, :, :H // 32], up_s[:, :, :H // 32]
     # down: untile -> [E, I_pad/4, H_pad] uint16 -> bytes [E, H_pad, I_pad/32, 16]
-    d = untile_down_blocks(down_blocks.view(torch.uint16), H_pad, I_pad)
+    d = untile_down_blocks(down_blocks.view(torch.int16), H_pad, I_pad)
     d = d.contiguous().view(torch.uint8).reshape(E, I_pad // 4, H_pad, 2)
     d = d.transpose(1, 2).contiguous().reshape(E, H_pad, I_pad // 32, 16)[:, :H, :I // 32]
     ds = untile_down_scale(down_scales, H_pad, I_pad).transpose(1, 2)[:, :H, :I // 32]
