@@ -30,11 +30,12 @@ PRENORM_LINEAR_TOPK_SCATTER_ACT = "prenorm_linear_topk_scatter_act"
 
 
 def apply_activation(activation, x: torch.Tensor) -> torch.Tensor:
-    """router.py:568-598."""
+    """router.py:568-598.  A 16-bit x is activated in fp32 and rounded once to its
+    dtype, the arithmetic of torch's CPU softmax / sigmoid on half tensors."""
     if activation == "softmax":
-        return F.softmax(x, dim=-1)
+        return F.softmax(x.float(), dim=-1).to(x.dtype)
     if activation == "sigmoid":
-        return torch.sigmoid(x)
+        return torch.sigmoid(x.float()).to(x.dtype)
     if callable(activation):
         return activation(x)
     raise ValueError(f"Unsupported activation function: {activation}")
@@ -49,9 +50,20 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 
 
 def _logits(x, w_he, bias, gamma, eps, cdt):
+    """router.py:422-426: F.linear of the operands cast to cdt.  For a 16-bit cdt it is
+    written out as what torch's CPU linear computes on the reference platform: the cast
+    operands' products summed in fp32, the cast bias added in fp32, one rounding to cdt
+    (bit-identical to F.linear on 99.8 % of outputs there, one rounding step apart on
+    the rest; the rounding of a half-precision CPU GEMM otherwise depends on the host's
+    BLAS path)."""
     if gamma is not None:
         x = rms_norm(x, gamma, eps)
-    return F.linear(x.to(cdt), w_he.T.to(cdt), bias.to(cdt) if bias is not None else None)
+    if cdt == torch.float32:
+        return F.linear(x.to(cdt), w_he.T.to(cdt), bias.to(cdt) if bias is not None else None)
+    acc = x.to(cdt).float() @ w_he.to(cdt).float()
+    if bias is not None:
+        acc = acc + bias.to(cdt).float()
+    return acc.to(cdt)
 
 
 def topk_act_scatter(x, w_he, k, bias=None, activation="softmax", gamma=None, eps=1e-6,
@@ -76,7 +88,9 @@ def act_topk_renorm_scatter(x, w_he, k, bias=None, activation="softmax", gamma=N
     logits = _logits(x, w_he, bias, gamma, eps, computation_dtype)
     probs = apply_activation(activation, logits)
     vals, idx = torch.topk(probs, k, dim=-1)
-    vals = vals / vals.sum(dim=-1, keepdim=True)
+    # sum and quotient in fp32, each rounded once to cdt (torch's half-tensor CPU ops)
+    s = vals.float().sum(dim=-1, keepdim=True).to(vals.dtype)
+    vals = (vals.float() / s.float()).to(vals.dtype)
     aff = torch.zeros(T, E, dtype=computation_dtype)
     aff.scatter_(1, idx, vals)
     return aff, logits

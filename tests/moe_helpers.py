@@ -49,8 +49,16 @@ def routing_agreement(layer, ref, x, dev):
     for t in torch.nonzero(bad).flatten().tolist():
         assert near_tie(logits_r[t], k)
     ok = ~bad
-    assert torch.allclose(aff_g[ok], aff_r[ok], rtol=2e-6, atol=1e-7)
+    aff_close(aff_g[ok], aff_r[ok], logits_g[ok], logits_r[ok], 1e-6)
     return aff_r, bad
+
+
+def aff_close(aff_g, aff_r, logits_g, logits_r, tol):
+    """Affinities within tol (one rounding step of the computation dtype below 1) plus the
+    token's largest logit difference (a softmax or sigmoid moves by less than its input)."""
+    dl = (logits_g.double() - logits_r.double()).abs().max(1, keepdim=True).values
+    d = (aff_g.double() - aff_r.double()).abs()
+    assert bool((d <= tol + dl).all()), float((d - tol - dl).max())
 
 
 def near_tie(scores, k, rel=1e-5):

@@ -1,6 +1,6 @@
 """Hardware behaviour the kernels rely on: MFMA operand/result layout and the CDNA4
-scaled fp4 -> bf16 conversion (its agreement with the reference dequant is recorded;
-the GEMM weights only use scale bytes 1..254)."""
+scaled fp4 -> bf16 conversion, which agrees with the reference dequant for every scale
+byte except 255 (the fused GEMMs run it; mxmoe_dequant_bf16 is bit-exact for all 256)."""
 
 import numpy as np
 import pytest
@@ -39,5 +39,7 @@ def test_hw_scaled_conversion_vs_reference(dev):
     same = (got == want).all(1)
     bad = [s for s in range(256) if not bool(same[s])]
     print("hardware conversion differs from the reference at scale bytes:", bad)
-    # the synthetic and real weight scales live well inside 1..253
-    assert all(s in (0, 254, 255) or s >= 253 for s in bad), bad
+    # Scale 255 (2^128) overflows fp32 in the reference (inf, and NaN for the zero codes);
+    # the hardware treats it otherwise.  Every other byte, the subnormal 2^-127 of byte 0
+    # and the overflowing products of bytes 253 and 254 included, agrees bit for bit.
+    assert bad == [255], bad
