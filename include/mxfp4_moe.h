@@ -253,6 +253,30 @@ int mxmoe_moe_block_decode(const uint16_t* x, const float* gamma, int64_t h_actu
                            void* stream);
 
 /*
+ * mxmoe_moe_block_decode without allocation or workspace argument.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).  The workspace
+ * is a device array of MXMOE_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held
+ * until the process ends; shapes whose mxmoe_moe_block_decode_workspace_bytes exceed it
+ * fail with MXMOE_E_WORKSPACE (GPT-OSS-120B at 64 tokens needs about 7 MB, E=256, top-8,
+ * H=7168, I=2048 at 128 tokens about 40 MB).  The calling thread's current device must
+ * be the stream's.  Calls that overlap on one GPU share the array and race: serialize
+ * them (one stream, or events).  Arguments and results as mxmoe_moe_block_decode.
+ */
+#define MXMOE_NOALLOC_SCRATCH_BYTES (48u << 20)
+int mxmoe_moe_block_decode_noalloc(const uint16_t* x, const float* gamma, int64_t h_actual,
+                                   float eps, const void* router_w, int router_w_dtype,
+                                   const void* router_b, int router_b_dtype, int router_act,
+                                   int act_before_topk, int renorm, float renorm_eps,
+                                   const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                                   const uint8_t* dn_s, const uint16_t* gu_bias,
+                                   const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I,
+                                   int64_t E, int top_k, int act, const float* clamps,
+                                   int scale_mode, uint16_t* out, float* logits_out,
+                                   int32_t* topk_idx_out, void* const* stage_events,
+                                   void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour
  * the kernels rely on.  mxmoe_probe_hw_dequant runs the CDNA4 scaled fp4->bf16
  * conversion the GEMMs use over blocks/scales like mxmoe_dequant_bf16;

@@ -54,6 +54,9 @@ _SIGNATURES = {
     "mxmoe_moe_block_decode": (_I, [_P, _P, _I64, _F, _P, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P,
                                     _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I, _P, _P,
                                     _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_block_decode_noalloc": (_I, [_P, _P, _I64, _F, _P, _I, _P, _I, _I, _I, _I, _F, _P,
+                                            _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I,
+                                            _P, _I, _P, _P, _P, _P, _P]),
     "mxmoe_probe_hw_dequant": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_probe_mfma": (_I, [_P, _P, _P, _P]),
 }

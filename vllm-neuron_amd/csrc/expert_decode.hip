@@ -17,6 +17,8 @@
 // Items are independent and each writes its own outputs.
 #include <math.h>
 
+#include <mutex>
+
 #include "capi_util.h"
 #include "common.h"
 #include "router_dev.h"
@@ -929,4 +931,74 @@ extern "C" int mxmoe_moe_block_decode(
                           dn_bias, T, H, I, E, top_k, act, clamps, scale_mode, out, logits_out,
                           topk_idx_out, workspace, dec, stage_events ? stage_events + 1 : nullptr,
                           stream);
+}
+
+// ---- The decode block without allocation: the workspace is a file-scope device array.
+//
+// Callers that cannot allocate (code under graph capture, tight serving loops) get the
+// same pipeline as mxmoe_moe_block_decode over a scratch array of fixed size in device
+// memory, which each GPU the library runs on holds until the process ends.  Every
+// buffer the pipeline reads in a call is written earlier in that call, so nothing needs
+// clearing between calls; calls that overlap on one GPU share the array and race.
+
+namespace mxmoe {
+
+static __device__ __align__(256) unsigned char scratch[MXMOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchMaxDevices = 64;
+static std::once_flag g_scratch_once[kScratchMaxDevices];
+static hipError_t g_scratch_rc[kScratchMaxDevices];
+static void* g_scratch_ptr[kScratchMaxDevices];
+
+// The current device's copy of the scratch array, looked up once per device with that
+// device current: in host code the array's name is not a device address.
+static int scratch_of_current_device(void** ptr) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(MXMOE_E_HIP, "moe_block_decode_noalloc: hipGetDevice: %s",
+                     hipGetErrorString(e));
+  MXMOE_REQUIRE(dev >= 0 && dev < kScratchMaxDevices,
+                "moe_block_decode_noalloc: device %d beyond the %d supported", dev,
+                kScratchMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_rc[dev] != hipSuccess)
+    return set_error(MXMOE_E_HIP, "moe_block_decode_noalloc: hipGetSymbolAddress: %s",
+                     hipGetErrorString(g_scratch_rc[dev]));
+  *ptr = g_scratch_ptr[dev];
+  return MXMOE_OK;
+}
+
+}  // namespace mxmoe
+
+extern "C" int mxmoe_moe_block_decode_noalloc(
+    const uint16_t* x, const float* gamma, int64_t h_actual, float eps, const void* router_w,
+    int router_w_dtype, const void* router_b, int router_b_dtype, int router_act,
+    int act_before_topk, int renorm, float renorm_eps, const uint8_t* gu_q, const uint8_t* gu_s,
+    const uint8_t* dn_q, const uint8_t* dn_s, const uint16_t* gu_bias, const uint16_t* dn_bias,
+    int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int act, const float* clamps,
+    int scale_mode, uint16_t* out, float* logits_out, int32_t* topk_idx_out,
+    void* const* stage_events, void* stream) {
+  clear_error();
+  int rc = tkg_check(T, H, I, E, top_k, act, scale_mode);
+  if (rc) return rc;
+  const size_t need = mxmoe_moe_block_decode_workspace_bytes(T, H, I, E, top_k);
+  if (need > (size_t)MXMOE_NOALLOC_SCRATCH_BYTES)
+    return set_error(MXMOE_E_WORKSPACE,
+                     "moe_block_decode_noalloc: T=%lld, H=%lld, I=%lld, E=%lld, top_k=%d need "
+                     "%zu bytes of scratch; the no-allocation entry point holds %zu",
+                     (long long)T, (long long)H, (long long)I, (long long)E, top_k, need,
+                     (size_t)MXMOE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  return mxmoe_moe_block_decode(x, gamma, h_actual, eps, router_w, router_w_dtype, router_b,
+                                router_b_dtype, router_act, act_before_topk, renorm, renorm_eps,
+                                gu_q, gu_s, dn_q, dn_s, gu_bias, dn_bias, T, H, I, E, top_k, act,
+                                clamps, scale_mode, out, logits_out, topk_idx_out, ws,
+                                (size_t)MXMOE_NOALLOC_SCRATCH_BYTES, stage_events, stream);
 }
