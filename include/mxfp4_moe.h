@@ -48,8 +48,10 @@ extern "C" {
 #define MXMOE_ACT_GELU 1
 #define MXMOE_ACT_SWISH 2 /* g * sigmoid(1.702 g) */
 
-#define MXMOE_SCALE_POST 0    /* out += y * affinity */
-#define MXMOE_SCALE_NO 1      /* out += y for selected experts */
+#define MXMOE_SCALE_POST 0         /* out += y * affinity */
+#define MXMOE_SCALE_NO 1           /* out += y for selected experts */
+#define MXMOE_SCALE_PRE 2          /* moe_cte: x * affinity before gate_up, bf16 sum of all experts */
+#define MXMOE_SCALE_PRE_DELAYED 3  /* moe_cte: act(g) * u * affinity before down, bf16 sum */
 
 #define MXMOE_ROUTER_SOFTMAX 0
 #define MXMOE_ROUTER_SIGMOID 1
@@ -163,21 +165,31 @@ int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* padding_mask
 
 /*
  * Prefill expert MLP over the blockwise mapping (grouped gate_up GEMM with fused
- * MXFP4 dequant, bias, clamps, activation; down GEMM with bias; affinity-weighted
- * combine in ascending expert order).  bf16 intermediates as in the reference.
+ * MXFP4 dequant, bias, clamps, activation; down GEMM with bias; combine).  bf16
+ * intermediates as in the reference.
  * Replaces: vllm_neuron/functional/moe/moe_cte.py:650-732 (_torch_compatible_moe_cte_kernel
  * -> nkilib moe_cte shard_on_block_mx); semantics of the torch flow at :448-581.
  * x bf16 [>=T, H]; affinities_masked fp32 [T*E]; gu_q/gu_s packed [E][2I x H];
  * dn_q/dn_s packed [E][H x I]; gu_bias bf16 [E, 2, I] or NULL; dn_bias bf16 [E, H]
- * or NULL; out [T, H] in bf16, or fp32 when out_f32 = 1 (the dtype of the reference
- * torch flow's result).  stage_events: NULL, or 4 hipEvent_t recorded on the stream
- * before the gate_up GEMM, after it, after the down GEMM and after the combine.
+ * or NULL; out [T, H] in bf16, or fp32 when out_f32 = 1.
+ * scale_mode:
+ *   MXMOE_SCALE_POST         out = sum of y * affinity over the routed experts, in
+ *                            ascending expert order, fp32 (:572-575);
+ *   MXMOE_SCALE_PRE          gate_up on bf16(x * affinity) (:518-520);
+ *   MXMOE_SCALE_PRE_DELAYED  the activation times bf16 affinity before the down GEMM
+ *                            (:556-558);
+ *   for both pre-scaling modes the affinity is taken as bf16 and out is the bf16 running
+ *   sum over ALL E experts in ascending order (:576-579): a routed expert adds its y, any
+ *   other expert expert_const[e] (bf16 [E, H]: its output for a zero input, i.e. the down
+ *   bias under PRE_SCALE_DELAYED and y_e(0) under PRE_SCALE; NULL adds nothing).
+ * stage_events: NULL, or 4 hipEvent_t recorded on the stream before the gate_up GEMM,
+ * after it, after the down GEMM and after the combine.
  */
 size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
-                                     int64_t block_size, int64_t n_blocks);
+                                     int64_t block_size, int64_t n_blocks, int scale_mode);
 int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked, const uint8_t* gu_q,
                   const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
-                  const uint16_t* gu_bias, const uint16_t* dn_bias,
+                  const uint16_t* gu_bias, const uint16_t* dn_bias, const uint16_t* expert_const,
                   const int32_t* token_position_to_id, const int32_t* block_to_expert,
                   int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I,
                   int64_t E, int act, const float* clamps, int scale_mode, int out_f32,

@@ -54,10 +54,15 @@ def test_argument_errors_are_reported():
     rc = lib.mxmoe_blockwise_mapping(dummy, None, 100, 8, 2, 64, 3, dummy, dummy, dummy, dummy,
                                      None, dummy, 1 << 20, None)
     assert rc == -1 and b"n_blocks" in lib.mxmoe_last_error()
-    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, dummy, dummy, 4,
-                           100, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30, None,
-                           None)
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, None, dummy,
+                           dummy, 4, 100, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
+                           None, None)
     assert rc == -1 and b"block_size" in lib.mxmoe_last_error()
+    # 32-bit activation-row offsets: slots x columns must stay below 4 GiB
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, None, dummy,
+                           dummy, 2048, 256, 64, 8192, 8192, 8, 2, None, 0, 0, dummy, dummy,
+                           1 << 40, None, None)
+    assert rc == -1 and b"4 GiB" in lib.mxmoe_last_error()
     rc = lib.mxmoe_moe_tkg(dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, None, 4, 2880,
                            2880, 32, 4, 2, None, 0, dummy, dummy, 10, None, None)
     assert rc == -3 and b"workspace" in lib.mxmoe_last_error()
@@ -67,8 +72,10 @@ def test_workspace_queries():
     from vllm_neuron_amd import _lib
 
     lib = _lib.load_library()
-    n = lib.mxmoe_moe_cte_workspace_bytes(4096, 2880, 2880, 128, 256, 191)
+    n = lib.mxmoe_moe_cte_workspace_bytes(4096, 2880, 2880, 128, 256, 191, 0)
     assert n >= 191 * 256 * 2880 * 2 * 2 + 4096 * 128 * 4
+    n_pre = lib.mxmoe_moe_cte_workspace_bytes(4096, 2880, 2880, 128, 256, 191, 2)
+    assert n_pre >= n + 191 * 256 * 2880 * 2  # the scaled rows of PRE_SCALE
     assert lib.mxmoe_moe_tkg_workspace_bytes(64, 2880, 2880, 128, 4) >= 256 * 2880 * 8
 
 

@@ -194,3 +194,86 @@ def test_moe_cte_block_sizes(dev, block):
                              up_clamp_upper_limit=7.0, up_clamp_lower_limit=-7.0,
                              activation_function="Swish")
     check_close(got, want, ties, f"moe_cte block {block}")
+
+
+@pytest.mark.parametrize("mode", ["PRE_SCALE", "PRE_SCALE_DELAYED"])
+@pytest.mark.parametrize("biases", [True, False])
+def test_moe_cte_prescale_modes(dev, mode, biases):
+    """moe_cte's pre-scaling modes against the oracle's dense torch flow (bf16 affinities,
+    the bf16 running sum over every expert, moe_cte.py:465-579).  Biases are scaled up so
+    that the experts a token does not route to (its y_e(0), or the down bias) are a
+    visible share of the output."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.weights import MXFP4Experts
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+    from oracle.layer import RefLayer
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 512, biases=biases)
+    lt = synthetic.layer_tensors(shape, 37, exp_range=(118, 122))
+    if biases:
+        lt.gate_up_bias = (lt.gate_up_bias.float() * 20).to(torch.bfloat16)
+        lt.down_bias = (lt.down_bias.float() * 20).to(torch.bfloat16)
+    ref = RefLayer(lt)
+    w = MXFP4Experts.from_checkpoint(lt.gate_up_blocks, lt.gate_up_scales, lt.down_blocks,
+                                     lt.down_scales, lt.gate_up_bias, lt.down_bias).to(dev)
+    T = 300
+    x = synthetic.tokens(37, T, ref.H)
+    aff, _ = ref.route(x)
+    aff16 = aff.to(torch.bfloat16)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff16.float().to(dev), 8, 2, 256)
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, b2e, 256, conditions=cond,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function="Swish", expert_affinities_scaling_mode=mode,
+                     gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                     up_clamp_lower_limit=-6.0).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff16.float(), 8, 2, 256)
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, am_r.to(torch.bfloat16), gu, ref.down, gb, db,
+                             gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                             up_clamp_lower_limit=-6.0, activation_function="Swish",
+                             expert_affinities_scaling_mode=mode)
+    assert got.dtype == torch.bfloat16 and want.dtype == torch.bfloat16
+    check_close(got.float(), want.float(), None, f"moe_cte {mode} biases={biases}")
+
+
+def test_moe_cte_out_of_range_expert_block_is_empty(dev):
+    """A block_to_expert entry outside [0, E) (the reference would raise IndexError on its
+    weights) computes nothing: its slots add no term, every other block is unchanged."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 256)
+    ref, layer, _ = build(shape, 38, dev, exp=(118, 122))
+    T = 200
+    x = synthetic.tokens(38, T, ref.H)
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), 8, 2, 256)
+    b2e_h = b2e.cpu()
+    first = int(b2e_h[0])  # block 0 holds expert b2e[0]'s first tokens
+    bad = b2e.clone()
+    bad[0] = 8 + 3
+    w = layer.w
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, bad, 256,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function="Swish", gate_clamp_upper_limit=7.0,
+                     up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0).cpu()
+    dropped = tp.cpu()[:256]
+    dropped = dropped[dropped >= 0]
+    aff_cut = aff.clone()
+    aff_cut[dropped, first] = 0.0
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, 8, 2, 256)
+    am_cut = aff_cut.reshape(-1, 1)
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, am_cut, gu, ref.down, gb, db, gate_clamp_upper_limit=7.0,
+                             up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0,
+                             activation_function="Swish")
+    assert len(dropped) > 0
+    check_close(got, want, ties, "moe_cte block with out-of-range expert")

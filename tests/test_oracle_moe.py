@@ -132,3 +132,55 @@ def test_lazy_layer_matches_eager():
     aff, _ = eager.route(x)
     assert torch.equal(eager.decode_routed(x, aff), lazy.decode_routed(x, aff))
     assert torch.equal(eager.prefill_routed(x, aff), lazy.prefill_routed(x, aff))
+
+
+def closed_form_pre(layer, x, aff, mode, routed_only=False):
+    """float64 algebra of the pre-scaling modes (moe_cte.py:465-495): every expert of every
+    token contributes; PRE_SCALE scales the hidden row by the affinity before gate/up,
+    PRE_SCALE_DELAYED the activation before down; no weighting after down.  routed_only
+    drops the experts a token does not route to (a plausible mistake)."""
+    xd = x.double()
+    gu = layer.gate_up.double()
+    I = layer.I
+    out = torch.zeros(x.shape[0], layer.H, dtype=torch.float64)
+    lim = torch.tensor(layer.limit, dtype=torch.float64)
+    for t in range(x.shape[0]):
+        for e in range(layer.E):
+            a = float(aff[t, e])
+            if routed_only and a == 0:
+                continue
+            z = ((a * xd[t]) if mode == oc.PRE_SCALE else xd[t]) @ gu[e] + layer.gu_bias[e].double()
+            g, u = torch.minimum(z[:I], lim), z[I:].clamp(-layer.limit + 1, layer.limit + 1)
+            h = u * g * torch.sigmoid(1.702 * g)
+            if mode == oc.PRE_SCALE_DELAYED:
+                h = h * a
+            out[t] += h @ layer.down[e].double() + layer.dn_bias[e].double()
+    return out
+
+
+@pytest.mark.parametrize("mode", [oc.PRE_SCALE, oc.PRE_SCALE_DELAYED])
+def test_prescale_modes_vs_closed_form(mode):
+    """The oracle's pre-scaling flows (bf16 affinities, bf16 running sum over all experts)
+    against the float64 algebra, with biases large enough that the contributions of the
+    experts a token does not route to are a visible share of the output."""
+    from oracle import blockwise as obw
+
+    lt, syn = _mini_layer(E=4, K=2, seed=11)
+    lt.gate_up_bias = lt.gate_up_bias * 50
+    lt.down_bias = lt.down_bias * 50
+    layer = RefLayer(lt)
+    x = syn.tokens(12, 24, layer.H)
+    aff, _ = layer.route(x)
+    aff = aff.to(torch.bfloat16)
+    aff_m, _, _, _ = obw.build_blockwise_mapping(aff.float(), layer.E, layer.K, 256)
+    gu, gb, db = layer._cte_args()
+    got = oc.torch_moe_impl(x, aff_m.to(torch.bfloat16), gu, layer.down, gb, db,
+                            activation_function=layer.act, expert_affinities_scaling_mode=mode,
+                            **layer.clamps)
+    assert got.dtype == torch.bfloat16
+    want = closed_form_pre(layer, x, aff.float(), mode)
+    mx, mean = rel_errs(got.float(), want)
+    assert mx < 3e-2 and mean < 1e-2, (mx, mean)
+    # the unrouted experts' share is far above that tolerance
+    routed = closed_form_pre(layer, x, aff.float(), mode, routed_only=True)
+    assert rel_errs(routed, want)[1] > 0.05

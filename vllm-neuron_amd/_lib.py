@@ -15,7 +15,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libmxmoe.so"
 
 ACT_SILU, ACT_GELU, ACT_SWISH = 0, 1, 2
-SCALE_POST, SCALE_NO = 0, 1
+SCALE_POST, SCALE_NO, SCALE_PRE, SCALE_PRE_DELAYED = 0, 1, 2, 3
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 
@@ -41,9 +41,9 @@ _SIGNATURES = {
     "mxmoe_blockwise_workspace_bytes": (_SZ, [_I64, _I64]),
     "mxmoe_blockwise_mapping": (_I, [_P, _P, _I64, _I64, _I, _I64, _I64, _P, _P, _P, _P, _P, _P,
                                      _SZ, _P]),
-    "mxmoe_moe_cte_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
-    "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
-                           _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_cte_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
+    "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                           _I64, _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
     "mxmoe_moe_tkg_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
                            _I, _P, _P, _SZ, _P, _P]),

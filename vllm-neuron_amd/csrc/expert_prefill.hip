@@ -68,6 +68,8 @@ struct PrefillArgs {
   int group;              // M-tiles scheduled together (divides n_mtiles)
   const int2* order;      // (first M-tile of a group, its expert) by rank (null: rank order,
                           // expert 0)
+  int E;                  // experts: a tile whose expert lies outside [0, E) computes nothing
+  int a_by_slot;          // gate_up reads row `slot` of a (pre-scaled rows), not the token's
   ExpertParams p;
 };
 
@@ -655,6 +657,7 @@ __global__ void __launch_bounds__(kPThreads)
     const int2 me = args.order[rank];
     mt = me.x + sub;
     e = me.y;
+    if (e < 0 || e >= args.E) return;  // a caller's out-of-range expert id: no tile
   }
   const int m0 = mt * kPM;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -667,8 +670,8 @@ __global__ void __launch_bounds__(kPThreads)
     // Byte offset of the row's activations.  Padding slots read a real row (token 0 / the
     // tile's first slot): an MFMA output column depends on its own slot only, and padding
     // columns are never stored.
-    const uint32_t arow =
-        GATE_UP ? (uint32_t)(tk >= 0 ? tk : 0) : (uint32_t)(tk >= 0 ? m0 + tid : m0);
+    const uint32_t arow = (GATE_UP && !args.a_by_slot) ? (uint32_t)(tk >= 0 ? tk : 0)
+                                                       : (uint32_t)(tk >= 0 ? m0 + tid : m0);
     s_rowoff[tid] = arow * (uint32_t)args.K * 2u;
     const unsigned long long real = __ballot(tk >= 0);
     if (lane == 0) s_lastw[wave] = real ? 64 * wave + 63 - __builtin_clzll(real) : -1;
@@ -909,6 +912,86 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
   }
 }
 
+// The affinity of slot p (token tk, expert e) as the reference's pre-scaling modes use it:
+// a bf16 tensor (moe_cte.py:518-520, 556-558 multiply bf16 hidden rows / intermediates by
+// it), so the fp32 value is rounded to bf16.
+__device__ __forceinline__ float slot_affinity_bf16(const float* __restrict__ aff, int tk, int e,
+                                                    int E) {
+  return round_bf16(aff[(size_t)tk * E + e]);
+}
+
+// PRE_SCALE: xs[p] = bf16(x[token(p)] * a(p)) for every real slot p (moe_cte.py:518-520);
+// padding slots are left as they are (the GEMM reads but never stores them).  One
+// workgroup per slot, 8 columns per thread.
+__global__ void __launch_bounds__(256) cte_prescale_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ aff,
+    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int B, int T, int E,
+    int H, uint16_t* __restrict__ xs) {
+  const int64_t p = blockIdx.x;
+  const int tk = tp2id[p];
+  const int e = b2e[p / B];
+  if (tk < 0 || tk >= T || e < 0 || e >= E) return;
+  const float a = slot_affinity_bf16(aff, tk, e, E);
+  for (int n = threadIdx.x * 8; n < H; n += 256 * 8) {
+    const u16x8 v = *reinterpret_cast<const u16x8*>(x + (size_t)tk * H + n);
+    u16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(bf16_bits_to_f32(v[i]) * a);
+    *reinterpret_cast<u16x8*>(xs + (size_t)p * H + n) = r;
+  }
+}
+
+// PRE_SCALE_DELAYED: h[p] = bf16(h[p] * a(p)) for every real slot (moe_cte.py:556-558).
+__global__ void __launch_bounds__(256) cte_scale_h_kernel(
+    uint16_t* __restrict__ h, const float* __restrict__ aff, const int32_t* __restrict__ tp2id,
+    const int32_t* __restrict__ b2e, int B, int T, int E, int I) {
+  const int64_t p = blockIdx.x;
+  const int tk = tp2id[p];
+  const int e = b2e[p / B];
+  if (tk < 0 || tk >= T || e < 0 || e >= E) return;
+  const float a = slot_affinity_bf16(aff, tk, e, E);
+  for (int n = threadIdx.x * 8; n < I; n += 256 * 8) {
+    u16x8 v = *reinterpret_cast<const u16x8*>(h + (size_t)p * I + n);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = f32_to_bf16_bits(bf16_bits_to_f32(v[i]) * a);
+    *reinterpret_cast<u16x8*>(h + (size_t)p * I + n) = v;
+  }
+}
+
+// Combine of the pre-scaling modes (moe_cte.py:576-579): out[t] = sum over ALL experts e
+// in ascending order of y_e, with the bf16 running sum of the reference (a bf16 output
+// tensor, each addition rounded).  A routed expert contributes its slot's y, any other
+// expert its output for a zero input, expert_const[e] (the down bias under
+// PRE_SCALE_DELAYED, y_e(0) under PRE_SCALE), or nothing when expert_const is null.
+// Grid (T, column chunks of 2048); 8 columns per thread.
+__global__ void __launch_bounds__(256) cte_combine_dense_bf16_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
+    const uint16_t* __restrict__ expert_const, int H, int E, int out_f32, void* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int n = blockIdx.y * 2048 + threadIdx.x * 8;
+  if (n >= H) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < E; ++e) {
+    const int slot = inv[(size_t)t * E + e];
+    const uint16_t* src = slot >= 0 ? y + (size_t)slot * H
+                                    : (expert_const ? expert_const + (size_t)e * H : nullptr);
+    if (!src) continue;
+    const u16x8 v = *reinterpret_cast<const u16x8*>(src + n);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = round_bf16(acc[i] + bf16_bits_to_f32(v[i]));
+  }
+  if (out_f32) {
+    float* o = static_cast<float*>(out) + (size_t)t * H + n;
+    *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  } else {
+    u16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(acc[i]);
+    *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(out) + (size_t)t * H + n) = r;
+  }
+}
+
 __global__ void fill_i32_k(int32_t* __restrict__ p, int64_t n, int32_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -919,16 +1002,18 @@ struct CteWs {
   uint16_t* y;
   int32_t* inv;
   int2* order;
+  uint16_t* xs;  // PRE_SCALE: the scaled activation row of every slot
 };
 
 static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
-                        int64_t n_slots, CteWs* w) {
+                        int64_t n_slots, int scale_mode, CteWs* w) {
   Carver cv(base, cap);
   CteWs c;
   c.h = cv.take<uint16_t>(n_slots * I);
   c.y = cv.take<uint16_t>(n_slots * H);
   c.inv = cv.take<int32_t>(T * E);
   c.order = cv.take<int2>(n_slots / kPM);
+  c.xs = cv.take<uint16_t>(scale_mode == MXMOE_SCALE_PRE ? n_slots * H : 0);
   if (w) *w = c;
   return cv.off + 256;
 }
@@ -938,14 +1023,16 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
 using namespace mxmoe;
 
 extern "C" size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
-                                                int64_t block_size, int64_t n_blocks) {
-  return cte_carve(nullptr, ~(size_t)0, T, H, I, E, block_size * n_blocks, nullptr);
+                                                int64_t block_size, int64_t n_blocks,
+                                                int scale_mode) {
+  return cte_carve(nullptr, ~(size_t)0, T, H, I, E, block_size * n_blocks, scale_mode, nullptr);
 }
 
 extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                              const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
                              const uint8_t* dn_s, const uint16_t* gu_bias,
-                             const uint16_t* dn_bias, const int32_t* token_position_to_id,
+                             const uint16_t* dn_bias, const uint16_t* expert_const,
+                             const int32_t* token_position_to_id,
                              const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
                              int64_t T, int64_t H, int64_t I, int64_t E, int act,
                              const float* clamps, int scale_mode, int out_f32, void* out,
@@ -962,17 +1049,25 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
                 "moe_cte: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
   MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_cte: unknown activation %d", act);
-  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
+  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO ||
+                    scale_mode == MXMOE_SCALE_PRE || scale_mode == MXMOE_SCALE_PRE_DELAYED,
                 "moe_cte: unsupported scale mode %d", scale_mode);
   const int64_t n_slots = n_blocks * block_size;
   MXMOE_REQUIRE(n_slots / kPM <= kOrderMaxTiles,
                 "moe_cte: %lld slots exceed the %d M-tiles of 128 slots one call schedules",
                 (long long)n_slots, kOrderMaxTiles);
-  const size_t need = cte_carve(nullptr, ~(size_t)0, T, H, I, E, n_slots, nullptr);
+  // The GEMMs address activation rows with 32-bit byte offsets from one base.
+  const int64_t kmax = H > I ? H : I;
+  MXMOE_REQUIRE(n_slots * kmax * 2 < ((int64_t)1 << 32) && T * H * 2 < ((int64_t)1 << 32),
+                "moe_cte: %lld slots x %lld columns (or %lld tokens) exceed the 4 GiB of "
+                "activation rows one call addresses",
+                (long long)n_slots, (long long)kmax, (long long)T);
+  const size_t need = cte_carve(nullptr, ~(size_t)0, T, H, I, E, n_slots, scale_mode, nullptr);
   if (workspace_bytes < need)
     return set_error(MXMOE_E_WORKSPACE, "moe_cte: workspace %zu < %zu", workspace_bytes, need);
   CteWs w;
-  cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, &w);
+  cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, scale_mode, &w);
+  const bool pre = scale_mode == MXMOE_SCALE_PRE, delayed = scale_mode == MXMOE_SCALE_PRE_DELAYED;
   hipStream_t s = as_stream(stream);
   auto mark = [&](int i) {
     mark_event(stage_events, i, s);
@@ -987,14 +1082,20 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.n_mtiles = (int)(n_slots / kPM);
   a.group = prefill_group_tiles(block_size);
   a.order = w.order;
+  a.E = (int)E;
+  a.a_by_slot = pre ? 1 : 0;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
   a.p.up_hi = clamps ? clamps[3] : INFINITY;
   a.p.act = act;
 
-  // gate_up: A = x (K = H), rows = 2I
-  a.a = x;
+  // gate_up: A = x (K = H), rows = 2I; under PRE_SCALE the scaled row of every slot
+  if (pre)
+    hipLaunchKernelGGL(cte_prescale_kernel, dim3((unsigned)n_slots), dim3(256), 0, s, x,
+                       affinities_masked, token_position_to_id, block_to_expert,
+                       (int)block_size, (int)T, (int)E, (int)H, w.xs);
+  a.a = pre ? w.xs : x;
   a.wq = gu_q;
   a.ws = gu_s;
   a.bias = gu_bias;
@@ -1009,8 +1110,13 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
                      dim3(kPThreads), 0, s, a);
   mark(1);
+  if (delayed)
+    hipLaunchKernelGGL(cte_scale_h_kernel, dim3((unsigned)n_slots), dim3(256), 0, s, w.h,
+                       affinities_masked, token_position_to_id, block_to_expert,
+                       (int)block_size, (int)T, (int)E, (int)I);
   // down: A = h (K = I), rows = H
   a.a = w.h;
+  a.a_by_slot = 0;
   a.wq = dn_q;
   a.ws = dn_s;
   a.bias = dn_bias;
@@ -1026,8 +1132,13 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   hipLaunchKernelGGL(cte_inverse_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
                      token_position_to_id, block_to_expert, n_slots, (int)block_size, (int)T,
                      (int)E, w.inv);
-  hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, s, w.y,
-                     w.inv, affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
+  if (pre || delayed)
+    hipLaunchKernelGGL(cte_combine_dense_bf16_kernel,
+                       dim3((unsigned)T, (unsigned)((H + 2047) / 2048)), dim3(256), 0, s, w.y,
+                       w.inv, expert_const, (int)H, (int)E, out_f32, out);
+  else
+    hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, s, w.y,
+                       w.inv, affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
   mark(3);
   return check_launch("moe_cte");
 }
@@ -1051,6 +1162,8 @@ extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, con
   a.H = (int)N;
   a.I = 0;
   a.B = kPM;
+  a.E = 1;
+  a.a_by_slot = 0;
   a.n_mtiles = (int)((M + kPM - 1) / kPM);
   a.n_ntiles = (int)((N / 16 + kPRG - 1) / kPRG);
   a.group = 1;

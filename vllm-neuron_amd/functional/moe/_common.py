@@ -24,12 +24,16 @@ def act_code(act) -> int:
     raise NotImplementedError(f"activation {name} has no MI355X kernel")
 
 
-def scale_code(mode, allow_no_scale: bool = True) -> int:
+def scale_code(mode, allow_no_scale: bool = True, allow_pre: bool = False) -> int:
     name = member_name(mode)
     if name == "POST_SCALE":
         return _lib.SCALE_POST
     if name == "NO_SCALE" and allow_no_scale:
         return _lib.SCALE_NO
+    if name == "PRE_SCALE" and allow_pre:
+        return _lib.SCALE_PRE
+    if name == "PRE_SCALE_DELAYED" and allow_pre:
+        return _lib.SCALE_PRE_DELAYED
     raise NotImplementedError(f"expert_affinities_scaling_mode {name} has no MI355X kernel")
 
 

@@ -15,9 +15,17 @@ The reference's own MX parameters (Trainium layout, model_mxfp4.py:957-1018, wit
 tiled bias views of :1408-1420) are accepted as they are and converted once per tensor
 version.
 
-expert_affinities_scaling_mode: POST_SCALE.  The reference torch flow's NO_SCALE adds
-the outputs of every expert for every token, routed or not (moe_cte.py:576-579), which
-a routed kernel does not compute; it raises NotImplementedError here.  Trainium tuning arguments (n_block_per_iter,
+expert_affinities_scaling_mode (moe_cte.py:465-495, 518-579):
+  * POST_SCALE: out = sum over the routed experts of y * affinity, fp32, ascending ids.
+  * PRE_SCALE / PRE_SCALE_DELAYED: the affinity multiplies the hidden row before gate_up
+    / the activation before down, and the output is the bf16 running sum over ALL E
+    experts (:576-579).  The torch flow runs these modes with bf16 affinities (its
+    einsums take one dtype), so the affinities are used rounded to bf16.  An expert a
+    token does not route to adds its output for a zero input: the down bias under
+    PRE_SCALE_DELAYED, and under PRE_SCALE y_e(0) = down(act(clamp(b_gate)) *
+    clamp(b_up)) + b_down, computed once per weight version by the same kernels.
+  * NO_SCALE: the torch flow adds every expert's full output for every token, routed or
+    not, which a routed kernel does not compute; it raises NotImplementedError.  Trainium tuning arguments (n_block_per_iter,
 block_sharding_strategy, n_static_blocks, n_dynamic_blocks, checkpoint_activation,
 skip_weight, ...) are accepted and have no effect; ``conditions`` is not needed
 because empty blocks are detected from token_position_to_id.
@@ -32,6 +40,7 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import MoECTEImplementation, QuantizationType, member_name
+from ._cache import derived
 from ._common import act_code, resolve_experts, scale_code
 
 
@@ -66,7 +75,7 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
         raise NotImplementedError("output_dtype must be bfloat16 or float32")
     if member_name(quantization_type) == "STATIC_MX":
         raise NotImplementedError("STATIC_MX (FP8 weights) has no MI355X kernel")
-    mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=False)
+    mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=False, allow_pre=True)
     if gate_up_activations_T is not None or down_activations is not None:
         raise NotImplementedError("activation checkpoint buffers are not supported")
     if gate_up_proj_scale is None or down_proj_scale is None:
@@ -97,17 +106,57 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
     aff = expert_affinities_masked.reshape(-1).to(torch.float32).contiguous()
     tp2id = token_position_to_id.reshape(-1).to(torch.int32).contiguous()
     b2e = block_to_expert.reshape(-1).to(torch.int32).contiguous()
+    clamp_vals = (gate_clamp_lower_limit, gate_clamp_upper_limit, up_clamp_lower_limit,
+                  up_clamp_upper_limit)
+    act = act_code(activation_function)
+    const = None
+    if mode == _lib.SCALE_PRE_DELAYED:
+        const = ex.dn_bias
+    elif mode == _lib.SCALE_PRE and ex.gu_bias is not None:
+        const = zero_input_outputs(ex, act, clamp_vals)
     out = torch.empty(T, H, dtype=output_dtype, device=dev)
+    _cte_call(x, aff, ex, const, tp2id, b2e, n_blocks, block_size, T, act, clamp_vals, mode,
+              out, stage_events)
+    return out
+
+
+def _cte_call(x, aff, ex, const, tp2id, b2e, n_blocks, block_size, T, act, clamp_vals, mode,
+              out, stage_events=None):
+    """mxmoe_moe_cte on prepared arguments; out [T, H] bf16 or fp32."""
+    dev = x.device
+    E, H, I = ex.E, ex.H, ex.I
     L = _lib.lib()
-    ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks), dev)
-    clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
-                               up_clamp_lower_limit, up_clamp_upper_limit)
+    ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks, mode),
+                        dev)
+    clamps = _lib.clamps_array(*clamp_vals)
     rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), ex.gu_q.contiguous().data_ptr(),
                          ex.gu_s.contiguous().data_ptr(), ex.dn_q.contiguous().data_ptr(),
                          ex.dn_s.contiguous().data_ptr(), _lib.ptr(ex.gu_bias),
-                         _lib.ptr(ex.dn_bias), tp2id.data_ptr(), b2e.data_ptr(), n_blocks,
-                         block_size, T, H, I, E, act_code(activation_function), clamps, mode,
-                         int(output_dtype == torch.float32), out.data_ptr(), ws.data_ptr(),
+                         _lib.ptr(ex.dn_bias), _lib.ptr(const), tp2id.data_ptr(), b2e.data_ptr(),
+                         n_blocks, block_size, T, H, I, E, act, clamps, mode,
+                         int(out.dtype == torch.float32), out.data_ptr(), ws.data_ptr(),
                          ws.numel(), _lib.event_array(stage_events), _lib.stream_handle(dev))
     _lib.check(rc, "mxmoe_moe_cte")
-    return out
+
+
+def zero_input_outputs(ex, act: int, clamp_vals) -> Tensor:
+    """bf16 [E, H]: each expert's output for an all-zero hidden row (what a PRE_SCALE token
+    that does not route to the expert adds, moe_cte.py:518-579).  Computed by the same
+    kernels on E zero rows, row e routed to expert e alone with affinity 1 (an exact
+    copy of y_e in the fp32 POST_SCALE combine), once per weight version and activation."""
+    tag = f"zero_input_outputs:{act}:{clamp_vals}"
+
+    def make():
+        from .moe_blockwise import build_blockwise_mapping
+
+        E, H = ex.E, ex.H
+        dev = ex.gu_q.device
+        aff = torch.eye(E, dtype=torch.float32, device=dev)
+        aff_m, tp2id, b2e, _ = build_blockwise_mapping(aff, E, 1, 256)
+        x0 = torch.zeros(E, H, dtype=torch.bfloat16, device=dev)
+        y = torch.empty(E, H, dtype=torch.float32, device=dev)
+        _cte_call(x0, aff_m.reshape(-1), ex, None, tp2id, b2e, b2e.numel(), 256, E, act,
+                  clamp_vals, _lib.SCALE_POST, y)
+        return y.to(torch.bfloat16)
+
+    return derived(tag, (ex.gu_q, ex.gu_s, ex.dn_q, ex.dn_s, ex.gu_bias, ex.dn_bias), make)
