@@ -18,6 +18,12 @@ around each stage of every timed step.  ``roofline`` covers the dominant kernel 
 the headline step (decode gate_up weight streaming: HBM bound); ``prefill.roofline``
 covers the prefill gate_up GEMM (MFMA bound, bf16 MFMA after in-register dequant).
 
+Before the per-kernel timing pass and again right before each timed region the step runs
+untimed for ``--settle`` seconds (0.3 by default; counts reported as ``settle_steps``): a
+GPU that has been idle reaches its steady clocks only after a few hundred milliseconds of
+work, and a short timed region otherwise measures the clock ramp.  The timed region is
+exactly the requested steps.
+
 ``cpu_baseline`` times the CPU oracle (a port of the reference's CPU flow: dense
 all-expert fp32 decode, dense all-expert bf16 prefill) on the host cores over a
 bounded sample of experts / tokens and scales linearly to the full workload.
@@ -62,6 +68,10 @@ def parse():
                     help="routing skew: router bias -s*log(1 + rank) over a random expert order")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time decode with eager launches")
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed steps after the warmup and again right before "
+                         "each timed region, so that the GPU runs at its steady clocks "
+                         "(0 disables)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three device copies of exactly 1 GiB (the reference "
                          "kernel that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -219,14 +229,29 @@ def main():
     def ev():
         return torch.cuda.Event(enable_timing=True)
 
+    def settle(step_fn, seconds):
+        """Untimed steps for ``seconds`` of wall time (the GPU leaves its idle clocks within
+        a few hundred milliseconds of sustained work); returns the steps run."""
+        n, end = 0, time.perf_counter() + seconds
+        while time.perf_counter() < end:
+            for _ in range(8):
+                n += step_fn(n)
+            torch.cuda.synchronize()
+        return n
+
+    def eager_step(n):
+        layers[n % L].decode(xs[n % L])
+        return 1
+
     # ---------------- decode
     for s in range(args.warmup):
         layers[s % L].decode(xs[s % L])
     torch.cuda.synchronize()
+    settled = settle(eager_step, args.settle)
 
     # Per-kernel durations: an eager pass with the library's stage events on the launch
     # stream (events recorded inside a captured graph do not time its kernels).
-    n_ev = min(args.steps, 100)
+    n_ev = 100
     stage = [[ev() for _ in range(6)] for _ in range(n_ev)]
     e0, e1 = ev(), ev()
     e0.record()
@@ -259,6 +284,10 @@ def main():
         except Exception as exc:  # capture unsupported: time eagerly
             print(f"graph capture failed ({exc}); timing eagerly", file=sys.stderr)
             torch.cuda.synchronize()
+    if mode == "hip-graph":
+        settled += settle(lambda n: (graph.replay(), G)[1], args.settle)
+    else:
+        settled += settle(eager_step, args.settle)
     t0, t1 = ev(), ev()
     if mode == "hip-graph":
         t0.record()
@@ -293,6 +322,7 @@ def main():
         "kernel_ms": {"router": rt_ms, "route": route_ms, "gate_up": gu_ms, "down": dn_ms,
                       "combine": cb_ms},
         "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
+        "settle_steps": settled, "settle_s": 2 * args.settle,
     }
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
     traffic, traffic_pre, traffic_src = measured_traffic(args.workload, dT, pT)
@@ -308,6 +338,7 @@ def main():
         for s in range(3):
             layers[s % L].prefill(xp[s % L])
         torch.cuda.synchronize()
+        p_settled = settle(lambda n: (layers[n % L].prefill(xp[n % L]), 1)[1], args.settle)
         ps = args.prefill_steps
         pst = [[ev() for _ in range(4)] for _ in range(ps)]
         p0, p1 = ev(), ev()
@@ -328,7 +359,8 @@ def main():
         t_min = max(pbytes / (HBM_PEAK_GBS * 1e9), flops / (MXFP4_PEAK_TFLOPS * 1e12))
         prefill = {
             "value": pT / (pms * 1e-3), "unit": "tokens/s", "ms_per_step": pms, "tokens": pT,
-            "steps": ps, "algorithmic_flops": flops, "algorithmic_bytes": pbytes,
+            "steps": ps, "settle_steps": p_settled, "algorithmic_flops": flops,
+            "algorithmic_bytes": pbytes,
             "layer_TFLOPs": flops / (pms * 1e-3) / 1e12,
             "layer_frac_mxfp4_peak": flops / (pms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS,
             "layer_frac_binding_roofline": t_min / (pms * 1e-3),
