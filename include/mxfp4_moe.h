@@ -270,8 +270,8 @@ int mxmoe_moe_block_decode(const uint16_t* x, const float* gamma, int64_t h_actu
  * graph capture, tight serving loops, harnesses that forbid allocation).  The workspace
  * is a device array of MXMOE_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held
  * until the process ends; shapes whose mxmoe_moe_block_decode_workspace_bytes exceed it
- * fail with MXMOE_E_WORKSPACE (GPT-OSS-120B at 64 tokens needs about 7 MB, E=256, top-8,
- * H=7168, I=2048 at 128 tokens about 40 MB).  The calling thread's current device must
+ * fail with MXMOE_E_WORKSPACE (GPT-OSS-120B at 64 tokens needs about 15 MiB, E=256,
+ * top-8, H=7168, I=2048 at 128 tokens about 38 MiB).  The calling thread's current device must
  * be the stream's.  Calls that overlap on one GPU share the array and race: serialize
  * them (one stream, or events).  Arguments and results as mxmoe_moe_block_decode.
  */
