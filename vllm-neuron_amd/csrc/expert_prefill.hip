@@ -165,21 +165,24 @@ __device__ __forceinline__ void prefill_rowoffs(const PrefillTile& p, uint32_t (
     ro[i] = PD == 0 ? p.a_off[i] : p.rowoff[(kPM / kPWaves) * wave + 4 * i + (lane >> 4)];
 }
 
+__device__ __forceinline__ void prefill_dma_one(uint8_t* sa, const PrefillTile& p, int c,
+                                                const uint32_t (&ro)[kPDma], int i) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+  const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
+  const int kcol = c * 128 + swz * 8;
+  const uint32_t off = ro[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
+  uint8_t* dst = sa + ((kPM / kPWaves) * wave + 4 * i) * 256;
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+               "s"(p.a)
+               : "memory", "m0");
+}
+
 __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, int c,
                                             const uint32_t (&ro)[kPDma]) {
-  const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < kPDma; ++i) {
-    const int swz = (lane & 15) ^ ((4 * i + (lane >> 4)) & 15);
-    const int kcol = c * 128 + swz * 8;
-    const uint32_t off = ro[i] + (kcol < p.K ? (uint32_t)kcol * 2u : 0u);
-    uint8_t* dst = sa + ((kPM / kPWaves) * wave + 4 * i) * 256;
-    const uint32_t lds = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
-                 "s"(p.a)
-                 : "memory", "m0");
-  }
+  for (int i = 0; i < kPDma; ++i) prefill_dma_one(sa, p, c, ro, i);
 }
 
 // The wave's weights and scales of chunk c (lanes past K re-read lane 0's bytes of the
@@ -192,24 +195,31 @@ __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, i
 // registers must therefore stay operands of a later wait (prefill_wait_b before use,
 // the loop's final drain for the last, unused refills), or the compiler could hand a
 // register still being loaded to another value.
-__device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p, int c) {
+// Load k of the chunk (k < kPRGW: row group k, else the scale word of quad k - kPRGW).
+__device__ __forceinline__ void prefill_load_b_one(PrefillB& f, const PrefillTile& p, int c,
+                                                   int k) {
   const int lane = threadIdx.x & 63;
   const bool ok = (c < p.nfull) || ((lane >> 4) < p.tail_q);
   const uint32_t lo = ok ? (uint32_t)lane : 0u;
-#pragma unroll
-  for (int r = 0; r < kPRGW; ++r) {
-    const uint32_t rr = r < p.rv ? r : p.rv - 1;
+  if (k < kPRGW) {
+    const uint32_t rr = k < p.rv ? k : p.rv - 1;
     const uint8_t* base = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u;
-    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(f.w[r]) : "v"(lo * 16u), "s"(base)
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(f.w[k]) : "v"(lo * 16u), "s"(base)
                  : "memory");
-  }
-#pragma unroll
-  for (int h = 0; h < kPRGW / 4; ++h) {
+  } else {
+    const int h = k - kPRGW;
     const uint32_t qq = 4 * h < p.rv ? h : 0;
     const uint8_t* sbase = p.ws + qq * (uint32_t)(2 * p.K) + (uint32_t)c * 256u;
     asm volatile("global_load_dword %0, %1, %2" : "=v"(f.s[h]) : "v"(lo * 4u), "s"(sbase)
                  : "memory");
   }
+}
+
+constexpr int kPLoadsB = kPRGW + kPRGW / 4;  // loads per chunk and wave: weights, scales
+
+__device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p, int c) {
+#pragma unroll
+  for (int k = 0; k < kPLoadsB; ++k) prefill_load_b_one(f, p, c, k);
 }
 
 // Waits until at most N vector memory operations issued after slot f's loads are
@@ -232,12 +242,19 @@ __device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
   }
 }
 
+struct NoHook {
+  __device__ void operator()(int) const {}
+};
+
 // acc[r][t] += W[row group r] x A[16-slot tile t] over chunk c.  Lanes past K get a zero
-// scale, so their weights add exact zeros.
-template <int NT, int PD>
+// scale, so their weights add exact zeros.  The compiler-scheduled loop (PD = 0) calls
+// hook(i) after the MFMAs of each (step j, fragment t), i = NT j + t: the caller issues its
+// loads for later chunks from there, between MFMA groups, instead of in one burst.
+template <int NT, int PD, typename Hook = NoHook>
 __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const PrefillB& f,
                                                 const PrefillTile& p, int c,
-                                                f32x4 (&acc)[kPRGW][NT]) {
+                                                f32x4 (&acc)[kPRGW][NT],
+                                                const Hook& hook = Hook()) {
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const bool kok = (c < p.nfull) || (q < p.tail_q);
   float sc[kPRGW];
@@ -261,6 +278,7 @@ __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const Prefill
             *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
 #pragma unroll
         for (int r = 0; r < kPRGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
+        hook(NT * j + t);
       }
     }
   } else {
@@ -321,10 +339,19 @@ __device__ __forceinline__ void prefill_barrier() {
 //    direct loads only: (P - 1) D at every step;
 //  - weights of chunk c: at most 2D + L later loads outstanding (exactly that from step
 //    2 on; steps 0 and 1 wait a little longer, once).
-constexpr int kPLoadsB = kPRGW + kPRGW / 4;
+// The compiler-scheduled loop (PD = 0, one lead chunk) issues the same loads in the same
+// order, spread between its MFMA groups: step c: [barrier] [wait] the MFMAs of chunk c
+// with direct load i of chunk c + 1 after MFMA group 2i (i < D) and weight load k of chunk
+// c + 2 after group 3 NT + k (k < L), once step j = 3 has dequantized the slot they refill.
+// The barrier counts are unchanged; the weights of chunk c then wait with D + L later
+// loads outstanding (exactly that from step 2 on, more at step 1; the same at step 0).
+// A wave that issues its loads in bursts leaves its MFMA slots idle while they issue; with
+// the loads between MFMA groups the two waves of a SIMD keep it busier (gate_up GEMM at
+// 4096 tokens of the 120B-shaped layer: about 5 % faster).
 constexpr int kPWaitFirst = (kPLead - 1) * kPDma;
 constexpr int kPWait = (kPLead - 1) * kPDma + kPLoadsB;
 constexpr int kPWaitB = 2 * kPDma + kPLoadsB;
+constexpr int kPWaitBSpread = kPDma + kPLoadsB;
 template <int S, int NT, bool ACTIVE, bool FIRST, int PD, typename Stage>
 __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
                                              const PrefillTile& p, int c,
@@ -332,6 +359,20 @@ __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2
   uint32_t ro[kPDma];
   prefill_rowoffs<PD>(p, ro);
   prefill_barrier<(FIRST || !ACTIVE) ? kPWaitFirst : kPWait>();
+  if constexpr (ACTIVE && PD == 0) {
+    static_assert(kPLead == 1 && 2 * kPDma <= 3 * NT, "spread loads: one lead chunk, "
+                  "direct loads before the weights");
+    uint8_t* next = stage(StageC<(S + 1) % kPStages>());
+    const int cn = min(c + 1, p.nc - 1), cw = min(c + 2, p.nc - 1);
+    prefill_wait_b<kPWaitBSpread>(f[S % 2]);
+    auto hook = [&](int i) {
+      if (i % 2 == 0 && i / 2 < kPDma) prefill_dma_one(next, p, cn, ro, i / 2);
+      if (i >= 3 * NT && i - 3 * NT < kPLoadsB) prefill_load_b_one(f[S % 2], p, cw, i - 3 * NT);
+    };
+    prefill_compute<NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc, hook);
+    __builtin_amdgcn_sched_barrier(0);
+    return;
+  }
   prefill_dma(stage(StageC<(S + kPLead) % kPStages>()), p, min(c + kPLead, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
