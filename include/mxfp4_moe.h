@@ -61,6 +61,12 @@ extern "C" {
 #define MXMOE_DT_F16 1
 #define MXMOE_DT_BF16 2
 
+/* Expert weight formats (weight_fmt arguments), both in this library's packed layout with
+ * E8M0 scales per 32 elements along K: MXFP4 (e2m1 pairs, [rows/16, 8K] bytes) and MXFP8
+ * (E4M3FN, [rows/16, 16K] bytes); the scales are packed alike ([ceil(rows/64), 2K]). */
+#define MXMOE_WFMT_MXFP4 0
+#define MXMOE_WFMT_MXFP8 1
+
 
 /* Library version (major*10000 + minor*100 + patch). */
 int mxmoe_version(void);
@@ -78,13 +84,22 @@ int mxmoe_dequant_bf16(const uint8_t* blocks, const uint8_t* scales, uint16_t* o
                        int64_t rows, int64_t K, void* stream);
 
 /*
- * Weight-only MXFP4 linear: y[M, N] = bf16(x[M, K] . W[N, K]^T), fp32 accumulation,
- * W packed.  Replaces one expert projection of the MXFP4 path as the reference CPU
- * flow computes it: dequantize at load (weight_loaders_bf16.py:264-316), then the bf16
- * matmul with fp32 accumulation (vllm_neuron/functional/moe/moe_cte.py:536-537).
+ * MXFP8 -> bf16: element = E4M3FN(code) x 2^(scale - 127), one rounding to bf16, scale byte
+ * 255 and the NaN codes -> NaN (the OCP MX definition; the reference names MXFP8 weights
+ * for moe_cte's MX kernel, moe_cte.py:136-138, with no CPU flow to follow).  codes
+ * [rows, K/32, 32] uint8, scales [rows, K/32] -> out bf16 [rows, K].
+ */
+int mxmoe_dequant_mxfp8_bf16(const uint8_t* codes, const uint8_t* scales, uint16_t* out,
+                             int64_t rows, int64_t K, void* stream);
+
+/*
+ * Weight-only MX linear: y[M, N] = bf16(x[M, K] . W[N, K]^T), fp32 accumulation, W packed
+ * in weight_fmt (MXMOE_WFMT_*).  Replaces one expert projection of the MX path as the
+ * reference CPU flow computes it: dequantize at load (weight_loaders_bf16.py:264-316), then
+ * the bf16 matmul with fp32 accumulation (vllm_neuron/functional/moe/moe_cte.py:536-537).
  */
 int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, const uint8_t* ws,
-                 int64_t N, int64_t K, uint16_t* y, void* stream);
+                 int weight_fmt, int64_t N, int64_t K, uint16_t* y, void* stream);
 
 /*
  * Router: logits = x . W^T (+ bias), top-k, activation, scatter.
@@ -170,8 +185,10 @@ int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* padding_mask
  * Replaces: vllm_neuron/functional/moe/moe_cte.py:650-732 (_torch_compatible_moe_cte_kernel
  * -> nkilib moe_cte shard_on_block_mx); semantics of the torch flow at :448-581.
  * x bf16 [>=T, H]; affinities_masked fp32 [T*E]; gu_q/gu_s packed [E][2I x H];
- * dn_q/dn_s packed [E][H x I]; gu_bias bf16 [E, 2, I] or NULL; dn_bias bf16 [E, H]
- * or NULL; out [T, H] in bf16, or fp32 when out_f32 = 1.
+ * dn_q/dn_s packed [E][H x I], both in weight_fmt (MXMOE_WFMT_MXFP4, or MXMOE_WFMT_MXFP8:
+ * the MxFP8 weights of the reference's shard_on_block_mx kernel, moe_cte.py:136-138);
+ * gu_bias bf16 [E, 2, I] or NULL; dn_bias bf16 [E, H] or NULL; out [T, H] in bf16, or
+ * fp32 when out_f32 = 1.
  * scale_mode:
  *   MXMOE_SCALE_POST         out = sum of y * affinity over the routed experts, in
  *                            ascending expert order, fp32 (:572-575);
@@ -188,7 +205,7 @@ int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* padding_mask
 size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                      int64_t block_size, int64_t n_blocks, int scale_mode);
 int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked, const uint8_t* gu_q,
-                  const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s,
+                  const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s, int weight_fmt,
                   const uint16_t* gu_bias, const uint16_t* dn_bias, const uint16_t* expert_const,
                   const int32_t* token_position_to_id, const int32_t* block_to_expert,
                   int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I,
@@ -291,12 +308,15 @@ int mxmoe_moe_block_decode_noalloc(const uint16_t* x, const float* gamma, int64_
 /*
  * Diagnostics (no counterpart in the reference): they pin the hardware behaviour
  * the kernels rely on.  mxmoe_probe_hw_dequant runs the CDNA4 scaled fp4->bf16
- * conversion the GEMMs use over blocks/scales like mxmoe_dequant_bf16;
+ * conversion the GEMMs use over blocks/scales like mxmoe_dequant_bf16, and
+ * mxmoe_probe_hw_dequant_fp8 the scaled fp8->bf16 one like mxmoe_dequant_mxfp8_bf16;
  * mxmoe_probe_mfma multiplies A bf16 [16, 32] by B^T (B bf16 [16, 32]) with one
  * v_mfma_f32_16x16x32_bf16 using the library's operand convention -> D fp32 [16, 16].
  */
 int mxmoe_probe_hw_dequant(const uint8_t* blocks, const uint8_t* scales, uint16_t* out,
                            int64_t rows, int64_t K, void* stream);
+int mxmoe_probe_hw_dequant_fp8(const uint8_t* codes, const uint8_t* scales, uint16_t* out,
+                               int64_t rows, int64_t K, void* stream);
 int mxmoe_probe_mfma(const uint16_t* a, const uint16_t* b, float* d, void* stream);
 
 #ifdef __cplusplus

@@ -54,12 +54,20 @@ def test_argument_errors_are_reported():
     rc = lib.mxmoe_blockwise_mapping(dummy, None, 100, 8, 2, 64, 3, dummy, dummy, dummy, dummy,
                                      None, dummy, 1 << 20, None)
     assert rc == -1 and b"n_blocks" in lib.mxmoe_last_error()
-    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, None, dummy,
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, 0, None, None, None, dummy,
                            dummy, 4, 100, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
                            None, None)
     assert rc == -1 and b"block_size" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, 2, None, None, None, dummy,
+                           dummy, 4, 256, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
+                           None, None)
+    assert rc == -1 and b"weight format" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_linear(dummy, 4, dummy, dummy, 5, 64, 64, dummy, None)
+    assert rc == -1 and b"weight format" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_dequant_mxfp8_bf16(dummy, dummy, dummy, 4, 48, None)
+    assert rc == -1 and b"multiple of 32" in lib.mxmoe_last_error()
     # 32-bit activation-row offsets: slots x columns must stay below 4 GiB
-    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, None, None, None, dummy,
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, 0, None, None, None, dummy,
                            dummy, 2048, 256, 64, 8192, 8192, 8, 2, None, 0, 0, dummy, dummy,
                            1 << 40, None, None)
     assert rc == -1 and b"4 GiB" in lib.mxmoe_last_error()

@@ -43,3 +43,30 @@ def test_hw_scaled_conversion_vs_reference(dev):
     # the hardware treats it otherwise.  Every other byte, the subnormal 2^-127 of byte 0
     # and the overflowing products of bytes 253 and 254 included, agrees bit for bit.
     assert bad == [255], bad
+
+
+def test_mxfp8_dequant_exact_and_hw_conversion(dev):
+    """MXFP8: the library's integer dequantization is bit-exact with the oracle's MX
+    definition for every (scale, code) pair; the CDNA4 scaled fp8 -> bf16 conversion the
+    MXFP8 GEMMs run is compared over the same grid (the scale bytes where it differs are
+    printed and must be extreme ones only)."""
+    from oracle import mxfp8 as o8
+    from vllm_neuron_amd.functional.mxfp4 import dequantize_mxfp8_to_bf16
+
+    codes = torch.arange(256, dtype=torch.uint8).reshape(1, 8, 32).expand(256, 8, 32).contiguous()
+    scales = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(256, 1).expand(256, 8)
+    scales = scales.contiguous()
+    want = o8.dequantize_mxfp8_to_bf16(codes, scales)
+    wnan = torch.isnan(want.float())
+    for hw in (False, True):
+        got = dequantize_mxfp8_to_bf16(codes.to(dev), scales.to(dev), _hw_probe=hw).cpu()
+        gnan = torch.isnan(got.float())
+        same = (got.view(torch.int16) == want.view(torch.int16)) | (gnan & wnan)
+        bad = [s for s in range(256) if not bool(same[s].all())]
+        print("hw" if hw else "exact", "dequant differs from the MX definition at scale bytes:",
+              bad)
+        if not hw:
+            assert bad == []
+        else:
+            # Every scale byte whose results are normal bf16 numbers agrees bit for bit.
+            assert all(s < 20 or s > 240 for s in bad), bad

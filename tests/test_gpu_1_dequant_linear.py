@@ -56,3 +56,28 @@ def test_linear(dev, M, N, K):
     print(f"linear {M}x{N}x{K}: bit-identical fraction {frac_exact:.5f}")
     assert frac_exact > 0.99
     assert (d.mean() / want.abs().mean()).item() < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 32), (37, 48, 96), (64, 80, 416), (300, 64, 2048),
+                                   (128, 5760, 2880)])
+def test_linear_mxfp8(dev, M, N, K):
+    """The GEMM kernel on MXFP8 weights (two row groups per wave, 32 B per lane and chunk,
+    partial last chunks and N-tiles) against x @ W^T with the oracle's MX dequantization."""
+    from oracle import mxfp8 as o8
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.functional import mxfp8_linear
+    from vllm_neuron_amd.weights import pack_mxfp8
+
+    codes, scales = synthetic.mxfp8_tensor(21 + N, N, K)
+    x = synthetic.normal_bf16(22 + M, (M, K))
+    want = o8.mxfp8_linear(x, codes, scales).float()
+    wq, ws = pack_mxfp8(codes, scales)
+    got = mxfp8_linear(x.to(dev), wq.to(dev), ws.to(dev)).float().cpu()
+    d = (got - want).abs()
+    w_abs = o8.dequantize_mxfp8_to_bf16(codes, scales).float().abs()
+    acc_bound = 2 * K * 2.0 ** -24 * (x.float().abs() @ w_abs.T)
+    ulp = torch.maximum(want.abs(), got.abs()) * 2.0 ** -7
+    assert torch.all(d <= ulp + acc_bound + 1e-30), d.max()
+    frac_exact = (d == 0).float().mean().item()
+    print(f"mxfp8 linear {M}x{N}x{K}: bit-identical fraction {frac_exact:.5f}")
+    assert frac_exact > 0.99

@@ -277,3 +277,71 @@ def test_moe_cte_out_of_range_expert_block_is_empty(dev):
                              activation_function="Swish")
     assert len(dropped) > 0
     check_close(got, want, ties, "moe_cte block with out-of-range expert")
+
+
+def _mxfp8_experts(seed, E, H, I):
+    """Random MXFP8 experts: packed GPU tensors (biases [E, 2, I] / [E, H]) and the oracle's
+    bf16 [E, H, 2, I] gate_up and [E, I, H] down weights, biases [E, 2, I] / [E, 1, H]."""
+    from oracle import mxfp8 as o8
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.weights import interleave_row_groups, pack_mxfp8
+
+    gc, gs = synthetic.mxfp8_tensor(seed, I, H, lead=(E,))
+    uc, us = synthetic.mxfp8_tensor(seed + 1, I, H, lead=(E,))
+    dc, ds = synthetic.mxfp8_tensor(seed + 2, H, I, lead=(E,))
+    gu_q, gu_s = pack_mxfp8(interleave_row_groups(gc, uc), interleave_row_groups(gs, us))
+    dn_q, dn_s = pack_mxfp8(dc, ds)
+    gate, up = o8.dequantize_mxfp8_to_bf16(gc, gs), o8.dequantize_mxfp8_to_bf16(uc, us)
+    gu_ref = torch.stack([gate.transpose(1, 2), up.transpose(1, 2)], 2).contiguous()
+    dn_ref = o8.dequantize_mxfp8_to_bf16(dc, ds).transpose(1, 2).contiguous()
+    gb = (synthetic.normal_bf16(seed + 3, (E, 2, I)).float() * 0.05).to(torch.bfloat16)
+    db = (synthetic.normal_bf16(seed + 4, (E, H)).float() * 0.05).to(torch.bfloat16)
+    return (gu_q, gu_s, dn_q, dn_s, gb, db), (gu_ref, dn_ref, gb, db.unsqueeze(1))
+
+
+@pytest.mark.parametrize("E,k,H,I,T,block", [(8, 2, 256, 512, 300, 256), (6, 2, 416, 288, 77, 128)])
+def test_moe_cte_mxfp8_weights(dev, E, k, H, I, T, block):
+    """moe_cte with MXFP8 expert weights (the MxFP8 format of the reference's
+    shard_on_block_mx kernel, moe_cte.py:136-138) against the oracle's dense torch flow
+    (moe_cte.py:448-581) on the weights the MX definition dequantizes to; partial K chunks
+    and N-tiles in the second case."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    (gu_q, gu_s, dn_q, dn_s, gb, db), (gu_ref, dn_ref, gb_ref, db_ref) = _mxfp8_experts(
+        71 + H, E, H, I)
+    x = synthetic.tokens(71, T, H)
+    logits = synthetic.normal_bf16(72, (T, E)).float()
+    top = torch.topk(logits, k, dim=1)
+    aff = torch.zeros(T, E).scatter_(1, top.indices, torch.softmax(top.values, 1))
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), E, k, block)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    got = NF.moe_cte(x.to(dev), am_g, mv(gu_q), mv(dn_q), tp, b2e, block, conditions=cond,
+                     gate_and_up_proj_bias=mv(gb), down_proj_bias=mv(db),
+                     gate_up_proj_scale=mv(gu_s), down_proj_scale=mv(dn_s),
+                     activation_function="Swish", skip_token=True,
+                     expert_affinities_scaling_mode="POST_SCALE", gate_clamp_upper_limit=7.0,
+                     up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, E, k, block)
+    want = oc.torch_moe_impl(x, am_r, gu_ref, dn_ref, gb_ref, db_ref,
+                             gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                             up_clamp_lower_limit=-6.0, activation_function="Swish")
+    check_close(got, want, None, f"moe_cte MXFP8 E={E} H={H} I={I}")
+
+
+def test_decode_rejects_mxfp8_weights(dev):
+    """The decode operators take MXFP4 experts only, as the reference's decode kernel does
+    (moe_tkg.py:48)."""
+    from vllm_neuron_amd import functional as NF
+
+    (gu_q, gu_s, dn_q, dn_s, gb, db), _ = _mxfp8_experts(5, 4, 256, 256)
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=dev)
+    aff = torch.zeros(4, 4, device=dev)
+    idx = torch.zeros(4, 2, dtype=torch.int32, device=dev)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    with pytest.raises(NotImplementedError, match="MXFP8"):
+        NF.moe_tkg(x, mv(gu_q), mv(dn_q), aff, idx, is_all_expert=False,
+                   expert_gate_up_weights_scale=mv(gu_s), expert_down_weights_scale=mv(dn_s))

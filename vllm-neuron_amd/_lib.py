@@ -18,6 +18,7 @@ ACT_SILU, ACT_GELU, ACT_SWISH = 0, 1, 2
 SCALE_POST, SCALE_NO, SCALE_PRE, SCALE_PRE_DELAYED = 0, 1, 2, 3
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+WFMT_MXFP4, WFMT_MXFP8 = 0, 1
 
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -30,7 +31,8 @@ _SIGNATURES = {
     "mxmoe_version": (_I, []),
     "mxmoe_last_error": (C.c_char_p, []),
     "mxmoe_dequant_bf16": (_I, [_P, _P, _P, _I64, _I64, _P]),
-    "mxmoe_linear": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _P]),
+    "mxmoe_dequant_mxfp8_bf16": (_I, [_P, _P, _P, _I64, _I64, _P]),
+    "mxmoe_linear": (_I, [_P, _I64, _P, _P, _I, _I64, _I64, _P, _P]),
     "mxmoe_router_workspace_bytes": (_SZ, [_I64, _I64]),
     "mxmoe_router_topk": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _I, _I, _I, _I, _F, _I,
                                _P, _P, _P, _P, _P, _SZ, _P]),
@@ -42,8 +44,8 @@ _SIGNATURES = {
     "mxmoe_blockwise_mapping": (_I, [_P, _P, _I64, _I64, _I, _I64, _I64, _P, _P, _P, _P, _P, _P,
                                      _SZ, _P]),
     "mxmoe_moe_cte_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
-    "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
-                           _I64, _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                           _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
     "mxmoe_moe_tkg_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
                            _I, _P, _P, _SZ, _P, _P]),
@@ -58,6 +60,7 @@ _SIGNATURES = {
                                             _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I,
                                             _P, _I, _P, _P, _P, _P, _P]),
     "mxmoe_probe_hw_dequant": (_I, [_P, _P, _P, _I64, _I64, _P]),
+    "mxmoe_probe_hw_dequant_fp8": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "mxmoe_probe_mfma": (_I, [_P, _P, _P, _P]),
 }
 

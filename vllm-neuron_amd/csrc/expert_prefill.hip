@@ -15,7 +15,7 @@
 //   preceded by a wait for the wave's own direct loads of the chunk about to be read
 //   only (a counted vmcnt, not the full drain of __syncthreads), keeps the weight and
 //   activation streams in flight across chunks.  (The ring depth, the waves and row
-//   groups per workgroup are the constants kPStages, kPWaves and kPRG below; four
+//   groups per workgroup are the constants kPStages, kPWaves and PFmt below; four
 //   stages of 512-row tiles with 8 waves, one workgroup per CU, measured 3 % slower.)
 //   M-tiles never straddle blocks (block_size % 128 == 0) so one tile has one expert;
 //   tiles whose 128 slots are all padding exit at once, and the waves run only the
@@ -47,12 +47,22 @@
 namespace mxmoe {
 
 constexpr int kPM = 128;      // slots per M-tile
-constexpr int kPRG = 16;      // row groups per N-tile (256 rows)
 constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
-constexpr int kPRGW = kPRG / kPWaves;         // row groups per wave (whole scale quads)
 constexpr int kPDma = kPM / kPWaves / 4;      // direct loads (1 KiB = 4 rows) per wave and chunk
-static_assert(kPRGW == 4 || kPRGW == 8, "a wave holds one or two quads of row groups");
+
+// Weight formats (MXMOE_WFMT_*): MXFP4 (e2m1 pairs, 16 B per lane, row group and 128-wide
+// chunk) and MXFP8 (E4M3FN, 32 B per lane in two 16-B halves).  A wave holds 4 row groups
+// of MXFP4 or 2 of MXFP8: both are four 16-B registers per chunk, so the register ring,
+// the load counts and the waits are the same; an N-tile is 256 or 128 rows.
+constexpr int kWFmt4 = 0, kWFmt8 = 1;
+template <int F>
+struct PFmt {
+  static constexpr int RGW = F == kWFmt8 ? 2 : 4;        // row groups per wave
+  static constexpr int RG = RGW * kPWaves;                // row groups per N-tile
+  static constexpr uint32_t BYTES_PER_K = F == kWFmt8 ? 16u : 8u;  // of a row group
+};
+constexpr int kPBw = 4;  // 16-B weight registers per chunk and wave
 constexpr int kPStages = 2;   // activation chunks in LDS (2 or 4)
 constexpr int kPLead = kPStages - 1;  // chunks the direct loads run ahead
 
@@ -128,14 +138,16 @@ struct PrefillTile {
   const uint8_t* ws;         // this wave's scale quad
   uint32_t rg_bytes;
   int rv;                    // valid row groups of this wave (<= 4)
+  int sbyte;                 // the wave's first row group in its scale quad (byte index)
   int K, nc, nfull, tail_q;
 };
 
-// One weight chunk of a wave in registers: kPRGW row groups x 16 B per lane, and the
-// 32-bit scale word of each quad of row groups.
+// One weight chunk of a wave in registers: kPBw x 16 B per lane (MXFP4: row group r in
+// w[r]; MXFP8: half h of row group r in w[2r + h]), and the 32-bit scale word of the
+// wave's quad of row groups.
 struct PrefillB {
-  u32x4 w[kPRGW];
-  uint32_t s[kPRGW / 4];
+  u32x4 w[kPBw];
+  uint32_t s[1];
 };
 
 // The activation stages are separate arrays of the kernel, chosen at compile time by a
@@ -187,7 +199,7 @@ __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, i
 
 // The wave's weights and scales of chunk c (lanes past K re-read lane 0's bytes of the
 // chunk, row groups past the tile re-read its last valid one, a quad past the tile the
-// first quad's scales), kPRGW + kPRGW / 4 loads.  They are issued
+// first quad's scales), kPLoadsB loads.  They are issued
 // from inline assembly, so the compiler does not track them: with direct-to-LDS loads
 // in flight as well it cannot count the wait for register loads and would drain every
 // load (s_waitcnt vmcnt(0)) before their first use.  The compiler takes the outputs as
@@ -195,31 +207,42 @@ __device__ __forceinline__ void prefill_dma(uint8_t* sa, const PrefillTile& p, i
 // registers must therefore stay operands of a later wait (prefill_wait_b before use,
 // the loop's final drain for the last, unused refills), or the compiler could hand a
 // register still being loaded to another value.
-// Load k of the chunk (k < kPRGW: row group k, else the scale word of quad k - kPRGW).
+// Load k of the chunk (k < kPBw: weight register k, else the scale word of the quad).
+// MXFP8: half h of chunk c of a row group at c * 2048 + h * 1024, or in a partial last
+// chunk of tq blocks at nfull * 2048 + h * 256 tq.
+template <int F>
 __device__ __forceinline__ void prefill_load_b_one(PrefillB& f, const PrefillTile& p, int c,
                                                    int k) {
   const int lane = threadIdx.x & 63;
   const bool ok = (c < p.nfull) || ((lane >> 4) < p.tail_q);
   const uint32_t lo = ok ? (uint32_t)lane : 0u;
-  if (k < kPRGW) {
-    const uint32_t rr = k < p.rv ? k : p.rv - 1;
-    const uint8_t* base = p.wq + rr * p.rg_bytes + (uint32_t)c * 1024u;
+  if (k < kPBw) {
+    const int r = F == kWFmt8 ? k >> 1 : k;
+    const uint32_t rr = r < p.rv ? r : p.rv - 1;
+    uint32_t coff;
+    if constexpr (F == kWFmt8) {
+      const uint32_t h = (uint32_t)(k & 1);
+      coff = c < p.nfull ? (uint32_t)c * 2048u + h * 1024u
+                         : (uint32_t)p.nfull * 2048u + h * 256u * (uint32_t)p.tail_q;
+    } else {
+      coff = (uint32_t)c * 1024u;
+    }
+    const uint8_t* base = p.wq + rr * p.rg_bytes + coff;
     asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(f.w[k]) : "v"(lo * 16u), "s"(base)
                  : "memory");
   } else {
-    const int h = k - kPRGW;
-    const uint32_t qq = 4 * h < p.rv ? h : 0;
-    const uint8_t* sbase = p.ws + qq * (uint32_t)(2 * p.K) + (uint32_t)c * 256u;
-    asm volatile("global_load_dword %0, %1, %2" : "=v"(f.s[h]) : "v"(lo * 4u), "s"(sbase)
+    const uint8_t* sbase = p.ws + (uint32_t)c * 256u;
+    asm volatile("global_load_dword %0, %1, %2" : "=v"(f.s[0]) : "v"(lo * 4u), "s"(sbase)
                  : "memory");
   }
 }
 
-constexpr int kPLoadsB = kPRGW + kPRGW / 4;  // loads per chunk and wave: weights, scales
+constexpr int kPLoadsB = kPBw + 1;  // loads per chunk and wave: weights, scales
 
+template <int F>
 __device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p, int c) {
 #pragma unroll
-  for (int k = 0; k < kPLoadsB; ++k) prefill_load_b_one(f, p, c, k);
+  for (int k = 0; k < kPLoadsB; ++k) prefill_load_b_one<F>(f, p, c, k);
 }
 
 // Waits until at most N vector memory operations issued after slot f's loads are
@@ -228,17 +251,32 @@ __device__ __forceinline__ void prefill_load_b(PrefillB& f, const PrefillTile& p
 template <int N>
 __device__ __forceinline__ void prefill_wait_b(PrefillB& f) {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  if constexpr (kPRGW == 4) {
-    asm volatile("s_waitcnt vmcnt(%5)"
-                 : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.s[0])
-                 : "n"(N)
-                 : "memory");
+  static_assert(kPBw == 4, "the operands below are the ring slot's registers");
+  asm volatile("s_waitcnt vmcnt(%5)"
+               : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.s[0])
+               : "n"(N)
+               : "memory");
+}
+
+// Eight MXFP8 (E4M3FN) bytes of two 32-bit words, times the block scale, to bf16 with the
+// CDNA4 scaled conversion (two elements per instruction, low 16-bit word first).
+__device__ __forceinline__ bf16x8 dequant8_fp8(uint32_t w0, uint32_t w1, float scale) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true);
+  bf16x8 r = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  return r;
+}
+
+// Row group r's eight weights of MFMA step j in the chunk held by f.
+template <int F>
+__device__ __forceinline__ bf16x8 prefill_deq(const PrefillB& f, int r, int j, float sc) {
+  if constexpr (F == kWFmt8) {
+    const u32x4& w = f.w[2 * r + (j >> 1)];
+    return dequant8_fp8(w[2 * (j & 1)], w[2 * (j & 1) + 1], sc);
   } else {
-    asm volatile("s_waitcnt vmcnt(%10)"
-                 : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.w[2]), "+v"(f.w[3]), "+v"(f.w[4]),
-                   "+v"(f.w[5]), "+v"(f.w[6]), "+v"(f.w[7]), "+v"(f.s[0]), "+v"(f.s[1])
-                 : "n"(N)
-                 : "memory");
+    return dequant8(f.w[r][j], sc);
   }
 }
 
@@ -250,17 +288,18 @@ struct NoHook {
 // scale, so their weights add exact zeros.  The compiler-scheduled loop (PD = 0) calls
 // hook(i) after the MFMAs of each (step j, fragment t), i = NT j + t: the caller issues its
 // loads for later chunks from there, between MFMA groups, instead of in one burst.
-template <int NT, int PD, typename Hook = NoHook>
+template <int F, int NT, int PD, typename Hook = NoHook>
 __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const PrefillB& f,
                                                 const PrefillTile& p, int c,
-                                                f32x4 (&acc)[kPRGW][NT],
+                                                f32x4 (&acc)[PFmt<F>::RGW][NT],
                                                 const Hook& hook = Hook()) {
+  constexpr int RGW = PFmt<F>::RGW;
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const bool kok = (c < p.nfull) || (q < p.tail_q);
-  float sc[kPRGW];
+  float sc[RGW];
 #pragma unroll
-  for (int r = 0; r < kPRGW; ++r)
-    sc[r] = kok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
+  for (int r = 0; r < RGW; ++r)
+    sc[r] = kok ? e8m0_to_f32((f.s[0] >> (8 * (p.sbyte + r))) & 0xffu) : 0.0f;
   // Per 32-wide step j: the row groups' weights dequantized once, then the NT activation
   // fragments against them.  The fragments are read from LDS PD steps (j, t) ahead, into
   // a rotating set of registers, so each read has the MFMAs of PD steps to land in.
@@ -269,15 +308,15 @@ __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const Prefill
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int blk = (4 * q + j) ^ (lane & 15);
-      bf16x8 wf[kPRGW];
+      bf16x8 wf[RGW];
 #pragma unroll
-      for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][j], sc[r]);
+      for (int r = 0; r < RGW; ++r) wf[r] = prefill_deq<F>(f, r, j, sc[r]);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const u32x4 xv =
             *reinterpret_cast<const u32x4*>(sa + (16 * t + (lane & 15)) * 256 + blk * 16);
 #pragma unroll
-        for (int r = 0; r < kPRGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
+        for (int r = 0; r < RGW; ++r) acc[r][t] = mfma16(wf[r], as_bf16x8(xv), acc[r][t]);
         hook(NT * j + t);
       }
     }
@@ -293,28 +332,28 @@ __device__ __forceinline__ void prefill_compute(const uint8_t* sa, const Prefill
     u32x4 xb[PD];
 #pragma unroll
     for (int i = 0; i < PD; ++i) xb[i] = frag(i);
-    bf16x8 wf[kPRGW];
+    bf16x8 wf[RGW];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       if (i % NT == 0) {
 #pragma unroll
-        for (int r = 0; r < kPRGW; ++r) wf[r] = dequant8(f.w[r][i / NT], sc[r]);
+        for (int r = 0; r < RGW; ++r) wf[r] = prefill_deq<F>(f, r, i / NT, sc[r]);
       }
       const u32x4 x = xb[i % PD];
       if (i + PD < NS) xb[i % PD] = frag(i + PD);
 #pragma unroll
-      for (int r = 0; r < kPRGW; ++r) acc[r][i % NT] = mfma16(wf[r], as_bf16x8(x), acc[r][i % NT]);
+      for (int r = 0; r < RGW; ++r) acc[r][i % NT] = mfma16(wf[r], as_bf16x8(x), acc[r][i % NT]);
     }
     // The compiler's scheduler would pull the reads back next to their MFMAs; these groups
     // keep the order: PD reads, then per step four MFMAs and the read PD steps ahead.
     __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
 #pragma unroll
     for (int i = 0; i < NS - PD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, kPRGW, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RGW, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 #pragma unroll
-    for (int i = 0; i < PD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, kPRGW, 0);
+    for (int i = 0; i < PD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, RGW, 0);
   }
 }
 
@@ -328,7 +367,7 @@ __device__ __forceinline__ void prefill_barrier() {
 }
 
 // One chunk: chunk c is in stage S % kPStages.  Issue order (the vmcnt arithmetic
-// depends on it), with D = kPDma direct loads and L = kPRGW + kPRGW / 4 weight and
+// depends on it), with D = kPDma direct loads and L = kPLoadsB weight and
 // scale loads per chunk and P = kPLead:
 // prologue: weights of chunks 0 and 1 (2 x L), direct loads of chunks 0 .. P - 1 (P x D);
 // step c: [barrier] direct loads of chunk c + P (D), [wait] the MFMAs of chunk c, the
@@ -352,10 +391,10 @@ constexpr int kPWaitFirst = (kPLead - 1) * kPDma;
 constexpr int kPWait = (kPLead - 1) * kPDma + kPLoadsB;
 constexpr int kPWaitB = 2 * kPDma + kPLoadsB;
 constexpr int kPWaitBSpread = kPDma + kPLoadsB;
-template <int S, int NT, bool ACTIVE, bool FIRST, int PD, typename Stage>
+template <int F, int S, int NT, bool ACTIVE, bool FIRST, int PD, typename Stage>
 __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2],
                                              const PrefillTile& p, int c,
-                                             f32x4 (&acc)[kPRGW][NT]) {
+                                             f32x4 (&acc)[PFmt<F>::RGW][NT]) {
   uint32_t ro[kPDma];
   prefill_rowoffs<PD>(p, ro);
   prefill_barrier<(FIRST || !ACTIVE) ? kPWaitFirst : kPWait>();
@@ -367,9 +406,9 @@ __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2
     prefill_wait_b<kPWaitBSpread>(f[S % 2]);
     auto hook = [&](int i) {
       if (i % 2 == 0 && i / 2 < kPDma) prefill_dma_one(next, p, cn, ro, i / 2);
-      if (i >= 3 * NT && i - 3 * NT < kPLoadsB) prefill_load_b_one(f[S % 2], p, cw, i - 3 * NT);
+      if (i >= 3 * NT && i - 3 * NT < kPLoadsB) prefill_load_b_one<F>(f[S % 2], p, cw, i - 3 * NT);
     };
-    prefill_compute<NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc, hook);
+    prefill_compute<F, NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc, hook);
     __builtin_amdgcn_sched_barrier(0);
     return;
   }
@@ -377,20 +416,20 @@ __device__ __forceinline__ void prefill_step(const Stage& stage, PrefillB (&f)[2
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
     prefill_wait_b<kPWaitB>(f[S % 2]);
-    prefill_compute<NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc);
+    prefill_compute<F, NT, PD>(stage(StageC<S % kPStages>()), f[S % 2], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
-    prefill_load_b(f[S % 2], p, min(c + 2, p.nc - 1));
+    prefill_load_b<F>(f[S % 2], p, min(c + 2, p.nc - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-template <int NT, bool ACTIVE, int PD, typename Stage>
+template <int F, int NT, bool ACTIVE, int PD, typename Stage>
 __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTile& p,
-                                             f32x4 (&acc)[kPRGW][NT]) {
+                                             f32x4 (&acc)[PFmt<F>::RGW][NT]) {
   PrefillB f[2];
   if constexpr (ACTIVE) {
-    prefill_load_b(f[0], p, 0);
-    prefill_load_b(f[1], p, min(1, p.nc - 1));
+    prefill_load_b<F>(f[0], p, 0);
+    prefill_load_b<F>(f[1], p, min(1, p.nc - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
   uint32_t ro[kPDma];
@@ -399,19 +438,19 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
   if constexpr (kPLead > 1) prefill_dma(stage(StageC<1>()), p, min(1, p.nc - 1), ro);
   if constexpr (kPLead > 2) prefill_dma(stage(StageC<2>()), p, min(2, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
-  prefill_step<0, NT, ACTIVE, true, PD>(stage, f, p, 0, acc);
+  prefill_step<F, 0, NT, ACTIVE, true, PD>(stage, f, p, 0, acc);
   int c = 1;
   for (; c + 4 <= p.nc; c += 4) {
-    prefill_step<1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
-    prefill_step<2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
-    prefill_step<3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
-    prefill_step<0, NT, ACTIVE, false, PD>(stage, f, p, c + 3, acc);
+    prefill_step<F, 1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
+    prefill_step<F, 2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
+    prefill_step<F, 3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
+    prefill_step<F, 0, NT, ACTIVE, false, PD>(stage, f, p, c + 3, acc);
   }
   if (c < p.nc) {
-    prefill_step<1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
+    prefill_step<F, 1, NT, ACTIVE, false, PD>(stage, f, p, c, acc);
     if (c + 1 < p.nc) {
-      prefill_step<2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
-      if (c + 2 < p.nc) prefill_step<3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
+      prefill_step<F, 2, NT, ACTIVE, false, PD>(stage, f, p, c + 1, acc);
+      if (c + 2 < p.nc) prefill_step<F, 3, NT, ACTIVE, false, PD>(stage, f, p, c + 2, acc);
     }
   }
   // The loads issued past the last chunk (clamped re-loads) land before the wave goes
@@ -471,10 +510,10 @@ __device__ __forceinline__ void prefill_dma_light(uint8_t* ring, int slot, const
 //    kLLead) L later loads are outstanding (exact at every step: BAR);
 //  - weights of chunk c: at most kLSlots D + (kLSlots - 1) L (exact from step kLSlots on,
 //    a little longer before).
-template <int SB, int NT, bool ACTIVE, int BAR>
+template <int F, int SB, int NT, bool ACTIVE, int BAR>
 __device__ __forceinline__ void prefill_step_light(uint8_t* ring, PrefillB (&f)[kLSlots],
                                                    const PrefillTile& p, int c,
-                                                   f32x4 (&acc)[kPRGW][NT]) {
+                                                   f32x4 (&acc)[PFmt<F>::RGW][NT]) {
   uint32_t ro[NT];
   prefill_rowoffs_light<NT>(p, ro);
   prefill_barrier<BAR>();
@@ -482,23 +521,23 @@ __device__ __forceinline__ void prefill_step_light(uint8_t* ring, PrefillB (&f)[
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (ACTIVE) {
     prefill_wait_b<kLSlots * NT + (kLSlots - 1) * kPLoadsB>(f[SB]);
-    prefill_compute<NT, NT>(ring + (c & (kLStages - 1)) * (16 * NT * 256), f[SB], p, c, acc);
+    prefill_compute<F, NT, NT>(ring + (c & (kLStages - 1)) * (16 * NT * 256), f[SB], p, c, acc);
     __builtin_amdgcn_sched_barrier(0);
-    prefill_load_b(f[SB], p, min(c + kLSlots, p.nc - 1));
+    prefill_load_b<F>(f[SB], p, min(c + kLSlots, p.nc - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-template <int NT, bool ACTIVE>
+template <int F, int NT, bool ACTIVE>
 __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillTile& p,
-                                                   f32x4 (&acc)[kPRGW][NT]) {
+                                                   f32x4 (&acc)[PFmt<F>::RGW][NT]) {
   constexpr int D = NT, L = ACTIVE ? kPLoadsB : 0, B0 = (kLLead - 1) * D;
   static_assert(B0 + kLLead * L < 64 && kLSlots * D + (kLSlots - 1) * L < 64, "vmcnt range");
   static_assert(kLSlots == 4, "the unrolled steps below cycle through four weight slots");
   PrefillB f[kLSlots];
   if constexpr (ACTIVE) {
 #pragma unroll
-    for (int s = 0; s < kLSlots; ++s) prefill_load_b(f[s], p, min(s, p.nc - 1));
+    for (int s = 0; s < kLSlots; ++s) prefill_load_b<F>(f[s], p, min(s, p.nc - 1));
   }
   __builtin_amdgcn_sched_barrier(0);
   uint32_t ro[NT];
@@ -508,32 +547,32 @@ __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillT
   __builtin_amdgcn_sched_barrier(0);
   // Steps 0 .. kLLead - 1 have their own barrier counts; nested, so that every path issues
   // the loads in the order the counts assume.
-  prefill_step_light<0, NT, ACTIVE, B0>(ring, f, p, 0, acc);
+  prefill_step_light<F, 0, NT, ACTIVE, B0>(ring, f, p, 0, acc);
   if (1 < p.nc) {
-    prefill_step_light<1, NT, ACTIVE, B0 + L>(ring, f, p, 1, acc);
+    prefill_step_light<F, 1, NT, ACTIVE, B0 + L>(ring, f, p, 1, acc);
     if (2 < p.nc) {
-      prefill_step_light<2, NT, ACTIVE, B0 + 2 * L>(ring, f, p, 2, acc);
+      prefill_step_light<F, 2, NT, ACTIVE, B0 + 2 * L>(ring, f, p, 2, acc);
       if (3 < p.nc) {
-        prefill_step_light<3, NT, ACTIVE, B0 + 3 * L>(ring, f, p, 3, acc);
+        prefill_step_light<F, 3, NT, ACTIVE, B0 + 3 * L>(ring, f, p, 3, acc);
         if (4 < p.nc) {
-          prefill_step_light<0, NT, ACTIVE, B0 + 4 * L>(ring, f, p, 4, acc);
+          prefill_step_light<F, 0, NT, ACTIVE, B0 + 4 * L>(ring, f, p, 4, acc);
           if (5 < p.nc) {
-            prefill_step_light<1, NT, ACTIVE, B0 + 5 * L>(ring, f, p, 5, acc);
+            prefill_step_light<F, 1, NT, ACTIVE, B0 + 5 * L>(ring, f, p, 5, acc);
             if (6 < p.nc) {
-              prefill_step_light<2, NT, ACTIVE, B0 + 6 * L>(ring, f, p, 6, acc);
+              prefill_step_light<F, 2, NT, ACTIVE, B0 + 6 * L>(ring, f, p, 6, acc);
               constexpr int BS = B0 + kLLead * L;
               int c = kLLead;
               for (; c + 4 <= p.nc; c += 4) {
-                prefill_step_light<3, NT, ACTIVE, BS>(ring, f, p, c, acc);
-                prefill_step_light<0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
-                prefill_step_light<1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
-                prefill_step_light<2, NT, ACTIVE, BS>(ring, f, p, c + 3, acc);
+                prefill_step_light<F, 3, NT, ACTIVE, BS>(ring, f, p, c, acc);
+                prefill_step_light<F, 0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
+                prefill_step_light<F, 1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
+                prefill_step_light<F, 2, NT, ACTIVE, BS>(ring, f, p, c + 3, acc);
               }
               if (c < p.nc) {
-                prefill_step_light<3, NT, ACTIVE, BS>(ring, f, p, c, acc);
+                prefill_step_light<F, 3, NT, ACTIVE, BS>(ring, f, p, c, acc);
                 if (c + 1 < p.nc) {
-                  prefill_step_light<0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
-                  if (c + 2 < p.nc) prefill_step_light<1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
+                  prefill_step_light<F, 0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
+                  if (c + 2 < p.nc) prefill_step_light<F, 1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
                 }
               }
             }
@@ -554,17 +593,17 @@ __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillT
 
 // gate_up epilogue: bias, clamps and the activation on the bf16-rounded accumulators
 // (the reference's bf16 intermediates), h = up * act(gate) stored as bf16.
-template <int ACT, int NT>
+template <int F, int ACT, int NT>
 __device__ __forceinline__ void gate_up_store(const PrefillArgs& args, const PrefillTile& p,
-                                              const f32x4 (&acc)[kPRGW][NT],
-                                              const float (&gb)[kPRGW / 2][4],
-                                              const float (&ub)[kPRGW / 2][4],
+                                              const f32x4 (&acc)[PFmt<F>::RGW][NT],
+                                              const float (&gb)[PFmt<F>::RGW / 2][4],
+                                              const float (&ub)[PFmt<F>::RGW / 2][4],
                                               const int32_t* stok, int m0, int rg_first) {
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const int I = args.I;
 #pragma unroll
-  for (int pp = 0; pp < kPRGW / 2; ++pp) {
+  for (int pp = 0; pp < PFmt<F>::RGW / 2; ++pp) {
     if (2 * pp >= p.rv) continue;
     const int P = rg_first / 2 + pp;  // pair index = 16 intermediate columns
     const int col0 = 16 * P + 4 * q;
@@ -591,21 +630,22 @@ __device__ __forceinline__ void gate_up_store(const PrefillArgs& args, const Pre
   }
 }
 
-template <bool GATE_UP, int NT, bool LIGHT, typename Stage>
+template <int F, bool GATE_UP, int NT, bool LIGHT, typename Stage>
 __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
                                             const PrefillArgs& args, const PrefillTile& p,
                                             const int32_t* stok, int m0, int e, int rg_first) {
-  f32x4 acc[kPRGW][NT];
+  constexpr int RGW = PFmt<F>::RGW;
+  f32x4 acc[RGW][NT];
 #pragma unroll
-  for (int r = 0; r < kPRGW; ++r)
+  for (int r = 0; r < RGW; ++r)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (LIGHT)
-    prefill_loop_light<NT, true>(ring, p, acc);
+    prefill_loop_light<F, NT, true>(ring, p, acc);
   else
     // LDS read-ahead distance: 4 steps (NT steps for 1-2 subtiles); the gate_up 8-subtile
     // loop has no registers left for it and keeps the compiler's schedule (0).
-    prefill_loop<NT, true, GATE_UP && NT == 8 ? 0 : (NT < 4 ? NT : 4)>(stage, p, acc);
+    prefill_loop<F, NT, true, GATE_UP && NT == 8 ? 0 : (NT < 4 ? NT : 4)>(stage, p, acc);
 
   const int lane = threadIdx.x & 63, q = lane >> 4;
   typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
@@ -616,9 +656,9 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
   const uint16_t* bsrc = args.bias ? args.bias : reinterpret_cast<const uint16_t*>(args.wq);
   if (GATE_UP) {
     const int I = args.I;
-    float gb[kPRGW / 2][4], ub[kPRGW / 2][4];
+    float gb[RGW / 2][4], ub[RGW / 2][4];
 #pragma unroll
-    for (int pp = 0; pp < kPRGW / 2; ++pp) {
+    for (int pp = 0; pp < RGW / 2; ++pp) {
       const int col0 = 16 * (rg_first / 2 + pp) + 4 * q;
       const bool ok = args.bias && 2 * pp < p.rv;
 #pragma unroll
@@ -631,23 +671,23 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
     }
     // The activation is uniform: one dispatch, then straight-line code per element.
     if (args.p.act == kSwish)
-      gate_up_store<kSwish>(args, p, acc, gb, ub, stok, m0, rg_first);
+      gate_up_store<F, kSwish>(args, p, acc, gb, ub, stok, m0, rg_first);
     else if (args.p.act == kSiLU)
-      gate_up_store<kSiLU>(args, p, acc, gb, ub, stok, m0, rg_first);
+      gate_up_store<F, kSiLU>(args, p, acc, gb, ub, stok, m0, rg_first);
     else
-      gate_up_store<kGELU>(args, p, acc, gb, ub, stok, m0, rg_first);
+      gate_up_store<F, kGELU>(args, p, acc, gb, ub, stok, m0, rg_first);
   } else {
     const int H = args.H;
-    float bb[kPRGW][4];
+    float bb[RGW][4];
 #pragma unroll
-    for (int r = 0; r < kPRGW; ++r) {
+    for (int r = 0; r < RGW; ++r) {
       const int n0 = 16 * (rg_first + r) + 4 * q;
       const bool ok = args.bias && r < p.rv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) bb[r][i] = bf16_bits_to_f32(bsrc[ok ? (size_t)e * H + n0 + i : 0]);
     }
 #pragma unroll
-    for (int r = 0; r < kPRGW; ++r) {
+    for (int r = 0; r < RGW; ++r) {
       if (r >= p.rv) continue;
       const int n0 = 16 * (rg_first + r) + 4 * q;
 #pragma unroll
@@ -667,10 +707,11 @@ __device__ __forceinline__ void prefill_run(const Stage& stage, uint8_t* ring,
   }
 }
 
-template <bool GATE_UP>
+template <bool GATE_UP, int F>
 __global__ void __launch_bounds__(kPThreads)
     __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_kernel(
         PrefillArgs args) {
+  constexpr int RGW = PFmt<F>::RGW, RG = PFmt<F>::RG;
   constexpr int kS23 = kPStages == 4 ? kPM * 256 : 16;  // stages 2 and 3 exist with 4 stages
   __shared__ __attribute__((aligned(1024))) uint8_t sa01[2][kPM * 256], sa2[kS23], sa3[kS23];
   __shared__ int32_t stok[kPM];
@@ -723,15 +764,16 @@ __global__ void __launch_bounds__(kPThreads)
 
   PrefillTile p;
   p.K = args.K;
-  p.rg_bytes = (uint32_t)p.K * 8u;
+  p.rg_bytes = (uint32_t)p.K * PFmt<F>::BYTES_PER_K;
   const int n_rg_total = args.N_rows / 16;
-  const int rg0 = nt * kPRG;  // a multiple of 4: the tile holds whole scale quads
-  const int rg_valid = min(kPRG, n_rg_total - rg0);
-  const int rg_first = rg0 + kPRGW * wave;
-  p.rv = min(kPRGW, rg_valid - kPRGW * wave);
+  const int rg0 = nt * RG;  // a multiple of 4: the tile holds whole scale quads
+  const int rg_valid = min(RG, n_rg_total - rg0);
+  const int rg_first = rg0 + RGW * wave;
+  p.rv = min(RGW, rg_valid - RGW * wave);
   const int rgw = p.rv > 0 ? rg_first : rg0;  // waves without rows point at valid data
   p.wq = args.wq + ((size_t)e * n_rg_total + rgw) * p.rg_bytes;
   p.ws = args.ws + ((size_t)e * ((n_rg_total + 3) / 4) + rgw / 4) * (size_t)(2 * p.K);
+  p.sbyte = rgw % 4;
   p.nc = (p.K + 127) / 128;
   p.nfull = p.K / 128;
   p.tail_q = (p.K % 128) / 32;
@@ -742,18 +784,18 @@ __global__ void __launch_bounds__(kPThreads)
     uint8_t* ring = &sa01[0][0];
     if (p.rv <= 0) {
       if (ntiles <= 1) {
-        f32x4 none[kPRGW][1];
-        prefill_loop_light<1, false>(ring, p, none);
+        f32x4 none[RGW][1];
+        prefill_loop_light<F, 1, false>(ring, p, none);
       } else {
-        f32x4 none[kPRGW][2];
-        prefill_loop_light<2, false>(ring, p, none);
+        f32x4 none[RGW][2];
+        prefill_loop_light<F, 2, false>(ring, p, none);
       }
       return;
     }
     if (ntiles <= 1)
-      prefill_run<GATE_UP, 1, true>(stage, ring, args, p, stok, m0, e, rg_first);
+      prefill_run<F, GATE_UP, 1, true>(stage, ring, args, p, stok, m0, e, rg_first);
     else
-      prefill_run<GATE_UP, 2, true>(stage, ring, args, p, stok, m0, e, rg_first);
+      prefill_run<F, GATE_UP, 2, true>(stage, ring, args, p, stok, m0, e, rg_first);
     return;
   }
 #pragma unroll
@@ -761,14 +803,14 @@ __global__ void __launch_bounds__(kPThreads)
   if (p.rv <= 0) {
     // No row groups in this tile for this wave: it still brings its share of the
     // activations and meets the barriers.
-    f32x4 none[kPRGW][1];
-    prefill_loop<1, false, 1>(stage, p, none);
+    f32x4 none[RGW][1];
+    prefill_loop<F, 1, false, 1>(stage, p, none);
     return;
   }
   if (ntiles <= 4)
-    prefill_run<GATE_UP, 4, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
+    prefill_run<F, GATE_UP, 4, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
   else
-    prefill_run<GATE_UP, 8, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
+    prefill_run<F, GATE_UP, 8, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
 }
 
 // The GEMMs schedule M-tiles in groups of G consecutive tiles of one block (G = the
@@ -1059,6 +1101,27 @@ static size_t cte_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   return cv.off + 256;
 }
 
+// N-tiles of a projection with `rows` output rows, and its launch, per weight format.
+static int prefill_ntiles(int64_t rows, int fmt) {
+  const int rg = fmt == kWFmt8 ? PFmt<kWFmt8>::RG : PFmt<kWFmt4>::RG;
+  return (int)((rows / 16 + rg - 1) / rg);
+}
+
+static void launch_prefill_gemm(bool gate_up, int fmt, const PrefillArgs& a, hipStream_t s) {
+  const dim3 g(prefill_grid(a.n_mtiles, a.n_ntiles, a.group));
+  if (fmt == kWFmt8) {
+    if (gate_up)
+      hipLaunchKernelGGL((prefill_gemm_kernel<true, kWFmt8>), g, dim3(kPThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((prefill_gemm_kernel<false, kWFmt8>), g, dim3(kPThreads), 0, s, a);
+  } else {
+    if (gate_up)
+      hipLaunchKernelGGL((prefill_gemm_kernel<true, kWFmt4>), g, dim3(kPThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((prefill_gemm_kernel<false, kWFmt4>), g, dim3(kPThreads), 0, s, a);
+  }
+}
+
 }  // namespace mxmoe
 
 using namespace mxmoe;
@@ -1071,7 +1134,7 @@ extern "C" size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I,
 
 extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                              const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
-                             const uint8_t* dn_s, const uint16_t* gu_bias,
+                             const uint8_t* dn_s, int weight_fmt, const uint16_t* gu_bias,
                              const uint16_t* dn_bias, const uint16_t* expert_const,
                              const int32_t* token_position_to_id,
                              const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
@@ -1090,6 +1153,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
                 "moe_cte: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
   MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_cte: unknown activation %d", act);
+  MXMOE_REQUIRE(weight_fmt == MXMOE_WFMT_MXFP4 || weight_fmt == MXMOE_WFMT_MXFP8,
+                "moe_cte: unknown weight format %d", weight_fmt);
   MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO ||
                     scale_mode == MXMOE_SCALE_PRE || scale_mode == MXMOE_SCALE_PRE_DELAYED,
                 "moe_cte: unsupported scale mode %d", scale_mode);
@@ -1143,13 +1208,12 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.out = w.h;
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
-  a.n_ntiles = (int)((2 * I / 16 + kPRG - 1) / kPRG);
+  a.n_ntiles = prefill_ntiles(2 * I, weight_fmt);
   hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
                      (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
                      (int)block_size, a.n_mtiles, a.group, (int)T, w.order);
   mark(0);
-  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
-                     dim3(kPThreads), 0, s, a);
+  launch_prefill_gemm(true, weight_fmt, a, s);
   mark(1);
   if (delayed)
     hipLaunchKernelGGL(cte_scale_h_kernel, dim3((unsigned)n_slots), dim3(256), 0, s, w.h,
@@ -1164,9 +1228,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.out = w.y;
   a.K = (int)I;
   a.N_rows = (int)H;
-  a.n_ntiles = (int)((H / 16 + kPRG - 1) / kPRG);
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
-                     dim3(kPThreads), 0, s, a);
+  a.n_ntiles = prefill_ntiles(H, weight_fmt);
+  launch_prefill_gemm(false, weight_fmt, a, s);
   mark(2);
   hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
                      T * E, -1);
@@ -1185,9 +1248,11 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
 }
 
 extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, const uint8_t* ws,
-                            int64_t N, int64_t K, uint16_t* y, void* stream) {
+                            int weight_fmt, int64_t N, int64_t K, uint16_t* y, void* stream) {
   clear_error();
   MXMOE_REQUIRE(x && wq && ws && y, "linear: null pointer");
+  MXMOE_REQUIRE(weight_fmt == MXMOE_WFMT_MXFP4 || weight_fmt == MXMOE_WFMT_MXFP8,
+                "linear: unknown weight format %d", weight_fmt);
   MXMOE_REQUIRE(M >= 0 && N >= 16 && N % 16 == 0 && K >= 32 && K % 32 == 0,
                 "linear: N=%lld must be a multiple of 16 and K=%lld of 32", (long long)N,
                 (long long)K);
@@ -1206,13 +1271,12 @@ extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, con
   a.E = 1;
   a.a_by_slot = 0;
   a.n_mtiles = (int)((M + kPM - 1) / kPM);
-  a.n_ntiles = (int)((N / 16 + kPRG - 1) / kPRG);
+  a.n_ntiles = prefill_ntiles(N, weight_fmt);
   a.group = 1;
   a.p.gate_lo = -INFINITY;
   a.p.gate_hi = INFINITY;
   a.p.up_lo = -INFINITY;
   a.p.up_hi = INFINITY;
-  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(prefill_grid(a.n_mtiles, a.n_ntiles, a.group)),
-                     dim3(kPThreads), 0, as_stream(stream), a);
+  launch_prefill_gemm(false, weight_fmt, a, as_stream(stream));
   return check_launch("linear");
 }

@@ -9,7 +9,7 @@
 namespace mxmoe {
 
 // logits[t, e] = sum_h x[t, h] * w[e, h] (+ bias[e]).  One workgroup = TT token tiles x
-// ET expert tiles of 16; its 4 waves split the 128-wide K chunks round-robin and
+// ET expert tiles of 16; its NW waves split the 128-wide K chunks round-robin and
 // reduce through LDS in a fixed order.  A = router rows (experts), B = tokens.
 // Operands are 16-bit (XF16 / WF16: fp16, else bf16), multiplied as OP says:
 //   kOpBF16   bf16 MFMA; fp16 weights are first rounded to bf16 (a cast to bf16)
@@ -18,11 +18,11 @@ namespace mxmoe {
 //             MFMAs: every product is exact, as in an fp32 matmul of the two
 // (products of two bf16 or two fp16 values are exact in fp32 as well).  The bias is
 // rounded to bias_rnd and the logit to logit_rnd (Dt; kF32 leaves them as they are).
-template <int TT, int ET, bool XF16, bool WF16, int OP>
-__global__ void __launch_bounds__(256) router_logits_kernel(
+template <int TT, int ET, int NW, bool XF16, bool WF16, int OP>
+__global__ void __launch_bounds__(64 * NW) router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const void* __restrict__ bias,
     int bias_dt, int bias_rnd, int logit_rnd, float* __restrict__ logits, int T, int H, int E) {
-  __shared__ f32x4 red[4][ET][TT][64];
+  __shared__ f32x4 red[NW][ET][TT][64];
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, r16 = lane & 15;
   const int t0 = blockIdx.x * 16 * TT, e0 = blockIdx.y * 16 * ET;
@@ -43,7 +43,7 @@ __global__ void __launch_bounds__(256) router_logits_kernel(
     for (int t = 0; t < TT; ++t) acc[e][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  for (int c = wave; c < nc; c += 4) {
+  for (int c = wave; c < nc; c += NW) {
     // Lanes past K in a partial last chunk feed zeros; every lane runs the MFMAs.
     const bool ok = (c < H / 128) || (q < tail_q);
     const int k0 = c * 128 + q * 32;
@@ -97,12 +97,12 @@ __global__ void __launch_bounds__(256) router_logits_kernel(
 #pragma unroll
     for (int t = 0; t < TT; ++t) red[wave][e][t][lane] = acc[e][t];
   __syncthreads();
-  // Each wave finishes a share of the (e, t) tiles: fixed summation order 0..3.
-  for (int idx = wave; idx < ET * TT; idx += 4) {
+  // Each wave finishes a share of the (e, t) tiles: fixed summation order 0..NW-1.
+  for (int idx = wave; idx < ET * TT; idx += NW) {
     const int e = idx / TT, t = idx % TT;
     f32x4 s = red[0][e][t][lane];
 #pragma unroll
-    for (int v = 1; v < 4; ++v) s += red[v][e][t][lane];
+    for (int v = 1; v < NW; ++v) s += red[v][e][t][lane];
     const int tok = t0 + 16 * t + r16;
     if (tok >= T) continue;
 #pragma unroll
@@ -183,12 +183,12 @@ extern "C" size_t mxmoe_router_workspace_bytes(int64_t, int64_t) { return 0; }
 
 namespace mxmoe {
 
-template <int TT, int ET>
+template <int TT, int ET, int NW>
 static void launch_logits(const RouterSpec& r, dim3 grid, float* logits, int T, int H, int E,
                           hipStream_t s) {
 #define MXMOE_LOGITS(XF, WF, OP)                                                              \
-  hipLaunchKernelGGL((router_logits_kernel<TT, ET, XF, WF, OP>), grid, dim3(256), 0, s, r.x, \
-                     r.w, r.bias, r.bias_dt, r.bias_rnd, r.logit_rnd, logits, T, H, E)
+  hipLaunchKernelGGL((router_logits_kernel<TT, ET, NW, XF, WF, OP>), grid, dim3(64 * NW), 0, s, \
+                     r.x, r.w, r.bias, r.bias_dt, r.bias_rnd, r.logit_rnd, logits, T, H, E)
   const bool xh = r.x_dt == kF16, wh = r.w_dt == kF16;
   if (r.op == kOpF16) {
     if (xh && wh) MXMOE_LOGITS(true, true, kOpF16);
@@ -239,12 +239,13 @@ int router_run(const RouterSpec& r, int64_t T, int64_t H, int64_t E, int top_k, 
   if (T == 0) return MXMOE_OK;
   if (T >= 1024 && E >= 64) {
     // 32 tokens x 64 experts per workgroup: 256 workgroups at 4096 tokens and 128 experts
-    // (64 x 64 tiles left half of the CUs idle: 34 -> 27 us with the top-k).
+    // (64 x 64 tiles left half of the CUs idle: 34 -> 27 us with the top-k; eight waves
+    // per workgroup on 32 x 32 or 16 x 64 tiles measured 11 % and 26 % slower).
     dim3 grid((unsigned)((T + 31) / 32), (unsigned)((E + 63) / 64));
-    launch_logits<2, 4>(r, grid, logits, (int)T, (int)H, (int)E, s);
+    launch_logits<2, 4, 4>(r, grid, logits, (int)T, (int)H, (int)E, s);
   } else {
     dim3 grid((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16));
-    launch_logits<1, 1>(r, grid, logits, (int)T, (int)H, (int)E, s);
+    launch_logits<1, 1, 4>(r, grid, logits, (int)T, (int)H, (int)E, s);
   }
   rc = check_launch("router_logits");
   if (rc) return rc;

@@ -5,11 +5,13 @@ from ..enums import (ActFnType, ExpertAffinityScaleMode, MoECTEImplementation,
                      QuantizationType, RouterActFnType, RouterComputationOrder)
 from .moe import (build_blockwise_mapping, moe_block_tkg, moe_cte, moe_tkg, num_blocks, rmsnorm,
                   rmsnorm_router_topk_tkg, router)
-from .mxfp4 import dequantize_mxfp4_to_bf16, mxfp4_linear
+from .mxfp4 import (dequantize_mxfp4_to_bf16, dequantize_mxfp8_to_bf16, mxfp4_linear,
+                    mxfp8_linear)
 
 __all__ = [
     "router", "build_blockwise_mapping", "moe_cte", "moe_tkg", "moe_block_tkg", "rmsnorm",
     "rmsnorm_router_topk_tkg", "num_blocks", "dequantize_mxfp4_to_bf16", "mxfp4_linear",
+    "dequantize_mxfp8_to_bf16", "mxfp8_linear",
     "ActFnType", "ExpertAffinityScaleMode", "MoECTEImplementation", "QuantizationType",
     "RouterActFnType", "RouterComputationOrder",
 ]

@@ -38,7 +38,9 @@ def scale_code(mode, allow_no_scale: bool = True, allow_pre: bool = False) -> in
 
 
 def expert_shapes(gu_q: Tensor, gu_s: Tensor, dn_q: Tensor, dn_s: Tensor):
-    """Packed weights -> (E, H, I), validating every shape."""
+    """Packed weights -> (E, H, I, weight format), validating every shape.  The scales give
+    H (2H bytes per quad row); the gate_up bytes per row group then tell MXFP4 (8H) from
+    MXFP8 (16H)."""
     for t, n in ((gu_q, "gate_up weight"), (gu_s, "gate_up scale"), (dn_q, "down weight"),
                  (dn_s, "down scale")):
         if t is None:
@@ -47,15 +49,22 @@ def expert_shapes(gu_q: Tensor, gu_s: Tensor, dn_q: Tensor, dn_s: Tensor):
             raise ValueError(f"{n}: expected a packed uint8 [E, rows/16, bytes] tensor, got "
                              f"{t.dtype} {tuple(t.shape)}")
     E = gu_q.shape[0]
-    H = gu_q.shape[2] // 8
+    H = gu_s.shape[2] // 2
     I = gu_q.shape[1] * 16 // 2
-    exp = {"gu_s": (E, (2 * I + 63) // 64, 2 * H), "dn_q": (E, H // 16, 8 * I),
+    if gu_q.shape[2] == 8 * H:
+        fmt, per_k = _lib.WFMT_MXFP4, 8
+    elif gu_q.shape[2] == 16 * H:
+        fmt, per_k = _lib.WFMT_MXFP8, 16
+    else:
+        raise ValueError(f"gate_up weight: {gu_q.shape[2]} bytes per row group fit neither "
+                         f"MXFP4 ({8 * H}) nor MXFP8 ({16 * H}) for H = {H}")
+    exp = {"gu_s": (E, (2 * I + 63) // 64, 2 * H), "dn_q": (E, H // 16, per_k * I),
            "dn_s": (E, (H + 63) // 64, 2 * I)}
     got = {"gu_s": tuple(gu_s.shape), "dn_q": tuple(dn_q.shape), "dn_s": tuple(dn_s.shape)}
     for k in exp:
         if exp[k] != got[k]:
             raise ValueError(f"packed weight shapes disagree: {k} is {got[k]}, expected {exp[k]}")
-    return E, H, I
+    return E, H, I, fmt
 
 
 def gate_up_bias(b: Optional[Tensor], E: int, I: int) -> Optional[Tensor]:
@@ -94,6 +103,7 @@ class Experts(NamedTuple):
     E: int
     H: int
     I: int
+    fmt: int = 0  # MXMOE_WFMT_*: 0 MXFP4, 1 MXFP8
 
 
 def is_neuron_layout(gate_up_weight: Tensor) -> bool:
@@ -153,10 +163,18 @@ def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
 def resolve_experts(gu_w: Tensor, gu_s: Optional[Tensor], dn_w: Tensor, dn_s: Optional[Tensor],
                     gu_b: Optional[Tensor], dn_b: Optional[Tensor]) -> Experts:
     """The expert arguments of moe_cte / moe_tkg / moe_block_tkg in either layout: this
-    build's packed MXFP4 (uint8, 3-D; biases [E, 2, I] and [E, H]) or the reference's
+    build's packed MXFP4 or MXFP8 (uint8, 3-D; biases [E, 2, I] and [E, H]) or the reference's
     Trainium kernel layout (converted once per tensor version, see _from_neuron_layout)."""
     if is_neuron_layout(gu_w):
         return _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b)
-    E, H, I = expert_shapes(gu_w, gu_s, dn_w, dn_s)
+    E, H, I, fmt = expert_shapes(gu_w, gu_s, dn_w, dn_s)
     return Experts(gu_w, gu_s, dn_w, dn_s, gate_up_bias(gu_b, E, I), down_bias(dn_b, E, H), E,
-                   H, I)
+                   H, I, fmt)
+
+
+def require_mxfp4(ex: Experts, what: str) -> None:
+    """The decode operators take MXFP4 experts only, as the reference's decode kernel does
+    (vllm_neuron/functional/moe/moe_tkg.py:48: "Currently only supports MXFP4 on Trn3")."""
+    if ex.fmt != _lib.WFMT_MXFP4:
+        raise NotImplementedError(f"{what}: MXFP8 expert weights are supported by moe_cte only "
+                                  "(the reference decode kernel supports MXFP4 only)")

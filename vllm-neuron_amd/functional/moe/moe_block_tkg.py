@@ -25,7 +25,7 @@ from torch import Tensor
 from ... import _lib
 from ...enums import ActFnType, ExpertAffinityScaleMode, RouterActFnType, member_name
 from ._cache import transposed_rows
-from ._common import act_code, resolve_experts, scale_code
+from ._common import act_code, require_mxfp4, resolve_experts, scale_code
 from .moe_tkg import moe_tkg_raw
 from .router import rms_norm, router_topk_raw
 
@@ -125,6 +125,7 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
     ex = resolve_experts(expert_gate_up_weights, expert_gate_up_weights_scale,
                          expert_down_weights, expert_down_weights_scale, expert_gate_up_bias,
                          expert_down_bias)
+    require_mxfp4(ex, "moe_block_tkg")
     E_L = ex.E
     fn = member_name(router_act_fn)
     if fn == "SOFTMAX":

@@ -131,7 +131,7 @@ def _cte_call(x, aff, ex, const, tp2id, b2e, n_blocks, block_size, T, act, clamp
     clamps = _lib.clamps_array(*clamp_vals)
     rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), ex.gu_q.contiguous().data_ptr(),
                          ex.gu_s.contiguous().data_ptr(), ex.dn_q.contiguous().data_ptr(),
-                         ex.dn_s.contiguous().data_ptr(), _lib.ptr(ex.gu_bias),
+                         ex.dn_s.contiguous().data_ptr(), ex.fmt, _lib.ptr(ex.gu_bias),
                          _lib.ptr(ex.dn_bias), _lib.ptr(const), tp2id.data_ptr(), b2e.data_ptr(),
                          n_blocks, block_size, T, H, I, E, act, clamps, mode,
                          int(out.dtype == torch.float32), out.data_ptr(), ws.data_ptr(),

@@ -21,7 +21,7 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import ExpertAffinityScaleMode, MoEAllToAllVStrategy, member_name
-from ._common import Experts, act_code, resolve_experts, scale_code
+from ._common import Experts, act_code, require_mxfp4, resolve_experts, scale_code
 
 
 def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, ex: Experts, act: int, clamps,
@@ -85,6 +85,7 @@ def moe_tkg(hidden_input: Tensor, expert_gate_up_weights: Tensor, expert_down_we
     ex = resolve_experts(expert_gate_up_weights, expert_gate_up_weights_scale,
                          expert_down_weights, expert_down_weights_scale, expert_gate_up_bias,
                          expert_down_bias)
+    require_mxfp4(ex, "moe_tkg")
     idx = expert_index.to(torch.int64)
     val = torch.gather(expert_affinities.to(torch.float32), 1, idx)
     if rank_id is not None:

@@ -66,6 +66,20 @@ def mxfp4_tensor(seed: int, rows: int, K: int, exp_lo: int = 120, exp_hi: int = 
     return blocks, scales
 
 
+def mxfp8_tensor(seed: int, rows: int, K: int, exp_lo: int = 117, exp_hi: int = 121, lead=()):
+    """OCP MXFP8 [..., rows, K/32, 32] E4M3FN codes + [..., rows, K/32] E8M0 scales; the codes
+    keep exponent fields 3..10 (magnitudes 2^-4 .. 2^3 x 1.875) with random signs and
+    mantissas, so that the scales set the range."""
+    G = K // 32
+    n = int(np.prod(lead, dtype=np.int64)) * rows * G * 32
+    raw = rand_bytes(seed, n)
+    e = 3 + (raw.astype(np.int64) >> 4) % 8
+    codes = ((raw & 0x80) | (e << 3) | (raw & 7)).astype(np.uint8)
+    sc = rand_ints(seed + 7919, n // 32, exp_lo, exp_hi).astype(np.uint8)
+    return (torch.from_numpy(codes).reshape(*lead, rows, G, 32),
+            torch.from_numpy(sc).reshape(*lead, rows, G))
+
+
 def zipf_bias(seed: int, E: int, s: float) -> torch.Tensor:
     perm = np.argsort(_raw(seed, E), kind="stable")
     rank = np.empty(E, dtype=np.int64)

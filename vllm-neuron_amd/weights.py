@@ -1,4 +1,5 @@
-"""Load-time weight preparation: checkpoint MXFP4 tensors -> the kernels' packed layout.
+"""Load-time weight preparation: checkpoint MXFP4 (and MXFP8) tensors -> the kernels'
+packed layout.
 
 The reference prepares its kernel-facing MXFP4 layout once at load
 (vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:243-885, a Trainium-specific
@@ -70,6 +71,91 @@ def pack_mxfp4(blocks: torch.Tensor, scales: torch.Tensor):
         raise ValueError("expected blocks [..., N, G, 16] and scales [..., N, G]")
     d, s = _pack_2d(blocks.reshape(-1, N, G, 16), scales.reshape(-1, N, G))
     return d.reshape(*lead, N // 16, G * 256), s.reshape(*lead, (N + 63) // 64, G * 64)
+
+
+def _pack_scales(scales: torch.Tensor) -> torch.Tensor:
+    """scales [L, N, G] -> the packed scale layout [L, ceil(N/64), 64G] (see the module
+    docstring); shared by MXFP4 and MXFP8."""
+    L, N, G = scales.shape
+    nq, nfull, tq = (N // 16 + 3) // 4, G // 4, G % 4
+    s = scales
+    if nq * 64 != N:
+        s = torch.cat([s, s.new_zeros(L, nq * 64 - N, G)], 1)
+    s = s.reshape(L, nq, 4, 16, G)  # quad, r, row, block
+    parts = []
+    if nfull:
+        sf = s[..., :4 * nfull].reshape(L, nq, 4, 16, nfull, 4)  # quad, r, row, c, kq
+        parts.append(sf.permute(0, 1, 4, 5, 3, 2).reshape(L, nq, nfull * 256))
+    if tq:
+        st = s[..., 4 * nfull:]  # quad, r, row, kq
+        parts.append(st.permute(0, 1, 4, 3, 2).reshape(L, nq, tq * 64))
+    return torch.cat(parts, -1).contiguous()
+
+
+def _unpack_scales(scale: torch.Tensor, N: int, G: int) -> torch.Tensor:
+    """Inverse of _pack_scales: [L, ceil(N/64), 64G] -> [L, N, G]."""
+    nq, nfull, tq = (N // 16 + 3) // 4, G // 4, G % 4
+    s = scale.reshape(-1, nq, G * 64)
+    L = s.shape[0]
+    outs = []
+    if nfull:
+        sf = s[:, :, :nfull * 256].reshape(L, nq, nfull, 4, 16, 4)  # quad, c, kq, row, r
+        outs.append(sf.permute(0, 1, 5, 4, 2, 3).reshape(L, nq, 4, 16, nfull * 4))
+    if tq:
+        st = s[:, :, nfull * 256:].reshape(L, nq, tq, 16, 4)  # quad, kq, row, r
+        outs.append(st.permute(0, 1, 4, 3, 2))
+    return torch.cat(outs, 4).reshape(L, nq * 64, G)[:, :N].contiguous()
+
+
+def pack_mxfp8(codes: torch.Tensor, scales: torch.Tensor):
+    """OCP MXFP8 codes [..., N, K/32, 32] (E4M3FN bytes) + scales [..., N, K/32] (E8M0) ->
+    packed (data [..., N/16, 16K], scale [..., ceil(N/64), 2K]).
+
+    data: chunk c of row group g at g*16K + c*2048, in two halves of 1 KiB (h = 0, 1:
+    elements 16h .. 16h + 15 of each 32-block, the operands of MFMA steps 2h and 2h + 1);
+    inside a half the 16 bytes of lane l are row 16g + l%16, K-block 4c + l//16.  A
+    partial last chunk of tq < 4 blocks keeps halves of 256 tq bytes (lanes l < 16 tq).
+    scale: as pack_mxfp4."""
+    if codes.dtype != torch.uint8 or scales.dtype != torch.uint8:
+        raise TypeError("MXFP8 codes and scales must be uint8")
+    lead = codes.shape[:-3]
+    N, G = codes.shape[-3], codes.shape[-2]
+    if codes.shape[-1] != 32 or tuple(scales.shape) != tuple(codes.shape[:-1]):
+        raise ValueError("expected codes [..., N, G, 32] and scales [..., N, G]")
+    if N % 16:
+        raise ValueError(f"row count {N} must be a multiple of 16")
+    c = codes.reshape(-1, N // 16, 16, G, 2, 16)  # L, rg, r, block, half, byte
+    L, nrg, nfull, tq = c.shape[0], N // 16, G // 4, G % 4
+    parts = []
+    if nfull:
+        cf = c[:, :, :, :4 * nfull].reshape(L, nrg, 16, nfull, 4, 2, 16)  # r, chunk, q, h, byte
+        parts.append(cf.permute(0, 1, 3, 5, 4, 2, 6).reshape(L, nrg, nfull * 2048))
+    if tq:
+        ct = c[:, :, :, 4 * nfull:]  # L, rg, r, tq, h, byte
+        parts.append(ct.permute(0, 1, 4, 3, 2, 5).reshape(L, nrg, tq * 512))
+    d = torch.cat(parts, -1).contiguous()
+    sc = _pack_scales(scales.reshape(-1, N, G))
+    return d.reshape(*lead, nrg, G * 512), sc.reshape(*lead, (N + 63) // 64, G * 64)
+
+
+def unpack_mxfp8(data: torch.Tensor, scale: torch.Tensor):
+    """Inverse of pack_mxfp8 -> codes [..., N, K/32, 32] and scales [..., N, K/32]."""
+    lead = data.shape[:-2]
+    nrg, nbytes = data.shape[-2], data.shape[-1]
+    G = nbytes // 512
+    nfull, tq = G // 4, G % 4
+    d = data.reshape(-1, nrg, nbytes)
+    L = d.shape[0]
+    outs = []
+    if nfull:
+        df = d[:, :, :nfull * 2048].reshape(L, nrg, nfull, 2, 4, 16, 16)  # c, h, q, r, byte
+        outs.append(df.permute(0, 1, 5, 2, 4, 3, 6).reshape(L, nrg, 16, nfull * 4, 2, 16))
+    if tq:
+        dt = d[:, :, nfull * 2048:].reshape(L, nrg, 2, tq, 16, 16)  # h, tq, r, byte
+        outs.append(dt.permute(0, 1, 4, 3, 2, 5))
+    c = torch.cat(outs, 3).reshape(*lead, nrg * 16, G, 32)
+    sc = _unpack_scales(scale, nrg * 16, G).reshape(*lead, nrg * 16, G)
+    return c.contiguous(), sc
 
 
 def packed_scale_shape(N: int, K: int):
