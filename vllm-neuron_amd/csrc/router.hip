@@ -43,11 +43,11 @@ __global__ void __launch_bounds__(64 * NW) router_logits_kernel(
     for (int t = 0; t < TT; ++t) acc[e][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  for (int c = wave; c < nc; c += NW) {
-    // Lanes past K in a partial last chunk feed zeros; every lane runs the MFMAs.
+  // Chunk c's operands (lanes past K in a partial last chunk feed zeros; every lane runs
+  // the MFMAs), loaded one chunk ahead of their MFMAs into the other register set.
+  auto load = [&](int c, u32x4 (&xv)[TT][4], u32x4 (&wv)[ET][4]) {
     const bool ok = (c < H / 128) || (q < tail_q);
     const int k0 = c * 128 + q * 32;
-    u32x4 xv[TT][4], wv[ET][4];
 #pragma unroll
     for (int t = 0; t < TT; ++t)
 #pragma unroll
@@ -58,6 +58,8 @@ __global__ void __launch_bounds__(64 * NW) router_logits_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         wv[e][j] = ok ? *reinterpret_cast<const u32x4*>(wr[e] + k0 + 8 * j) : zero4;
+  };
+  auto mma = [&](const u32x4 (&xv)[TT][4], const u32x4 (&wv)[ET][4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -91,6 +93,17 @@ __global__ void __launch_bounds__(64 * NW) router_logits_kernel(
           for (int t = 0; t < TT; ++t) acc[e][t] = mfma16(a, as_bf16x8(xv[t][j]), acc[e][t]);
         }
       }
+  };
+  u32x4 xa[TT][4], wa[ET][4], xb[TT][4], wb[ET][4];
+  int c = wave;
+  if (c < nc) load(c, xa, wa);
+  for (; c < nc; c += 2 * NW) {
+    const int c1 = c + NW;
+    if (c1 < nc) load(c1, xb, wb);
+    mma(xa, wa);
+    if (c1 >= nc) break;
+    if (c1 + NW < nc) load(c1 + NW, xa, wa);
+    mma(xb, wb);
   }
 #pragma unroll
   for (int e = 0; e < ET; ++e)
