@@ -40,6 +40,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "capi_util.h"
 #include "common.h"
@@ -471,7 +472,7 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
 // 64 KB the full tiles use as two stages, kLLead chunks ahead; the weights go through a
 // ring of kLSlots register chunks (their accumulators leave the registers free), kLSlots
 // chunks ahead.  Wave w brings rows 4 (w + 4j) .. 4 (w + 4j) + 3, j < NT.
-constexpr int kLLead = 7, kLStages = 8, kLSlots = 4;
+constexpr int kLLead = 7, kLStages = 8, kLSlots = 8;
 static_assert(kLStages > kLLead && (kLStages & (kLStages - 1)) == 0, "light ring");
 
 template <int NT>
@@ -528,12 +529,40 @@ __device__ __forceinline__ void prefill_step_light(uint8_t* ring, PrefillB (&f)[
   }
 }
 
+// Steps c + I .. c + N - 1 of the light loop, chunk c + i in weight slot (S0 + i) %
+// kLSlots with barrier count B + i DB, nested so that a step runs only after the one
+// before it and then() only after all of them (every path of the control flow issues the
+// loads in the order the counts assume).
+template <int F, int NT, bool ACTIVE, int S0, int B, int DB, int I, int N, typename Then>
+__device__ __forceinline__ void prefill_light_tail(uint8_t* ring, PrefillB (&f)[kLSlots],
+                                                   const PrefillTile& p, int c,
+                                                   f32x4 (&acc)[PFmt<F>::RGW][NT],
+                                                   const Then& then) {
+  if constexpr (I < N) {
+    if (c + I < p.nc) {
+      prefill_step_light<F, (S0 + I) % kLSlots, NT, ACTIVE, B + I * DB>(ring, f, p, c + I, acc);
+      prefill_light_tail<F, NT, ACTIVE, S0, B, DB, I + 1, N>(ring, f, p, c, acc, then);
+    }
+  } else {
+    then();  // every step ran
+  }
+}
+
+// kLSlots steps c .. c + kLSlots - 1 (all run), slot (S0 + i) % kLSlots, barrier count B.
+template <int F, int NT, bool ACTIVE, int S0, int B, int... Is>
+__device__ __forceinline__ void prefill_light_block(uint8_t* ring, PrefillB (&f)[kLSlots],
+                                                    const PrefillTile& p, int c,
+                                                    f32x4 (&acc)[PFmt<F>::RGW][NT],
+                                                    std::integer_sequence<int, Is...>) {
+  (prefill_step_light<F, (S0 + Is) % kLSlots, NT, ACTIVE, B>(ring, f, p, c + Is, acc), ...);
+}
+
 template <int F, int NT, bool ACTIVE>
 __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillTile& p,
                                                    f32x4 (&acc)[PFmt<F>::RGW][NT]) {
   constexpr int D = NT, L = ACTIVE ? kPLoadsB : 0, B0 = (kLLead - 1) * D;
   static_assert(B0 + kLLead * L < 64 && kLSlots * D + (kLSlots - 1) * L < 64, "vmcnt range");
-  static_assert(kLSlots == 4, "the unrolled steps below cycle through four weight slots");
+  static_assert(kLSlots == kLStages && kLLead + 1 == kLSlots, "slots and slices cycle together");
   PrefillB f[kLSlots];
   if constexpr (ACTIVE) {
 #pragma unroll
@@ -545,42 +574,18 @@ __device__ __forceinline__ void prefill_loop_light(uint8_t* ring, const PrefillT
 #pragma unroll
   for (int v = 0; v < kLLead; ++v) prefill_dma_light<NT>(ring, v, p, min(v, p.nc - 1), ro);
   __builtin_amdgcn_sched_barrier(0);
-  // Steps 0 .. kLLead - 1 have their own barrier counts; nested, so that every path issues
-  // the loads in the order the counts assume.
-  prefill_step_light<F, 0, NT, ACTIVE, B0>(ring, f, p, 0, acc);
-  if (1 < p.nc) {
-    prefill_step_light<F, 1, NT, ACTIVE, B0 + L>(ring, f, p, 1, acc);
-    if (2 < p.nc) {
-      prefill_step_light<F, 2, NT, ACTIVE, B0 + 2 * L>(ring, f, p, 2, acc);
-      if (3 < p.nc) {
-        prefill_step_light<F, 3, NT, ACTIVE, B0 + 3 * L>(ring, f, p, 3, acc);
-        if (4 < p.nc) {
-          prefill_step_light<F, 0, NT, ACTIVE, B0 + 4 * L>(ring, f, p, 4, acc);
-          if (5 < p.nc) {
-            prefill_step_light<F, 1, NT, ACTIVE, B0 + 5 * L>(ring, f, p, 5, acc);
-            if (6 < p.nc) {
-              prefill_step_light<F, 2, NT, ACTIVE, B0 + 6 * L>(ring, f, p, 6, acc);
-              constexpr int BS = B0 + kLLead * L;
-              int c = kLLead;
-              for (; c + 4 <= p.nc; c += 4) {
-                prefill_step_light<F, 3, NT, ACTIVE, BS>(ring, f, p, c, acc);
-                prefill_step_light<F, 0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
-                prefill_step_light<F, 1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
-                prefill_step_light<F, 2, NT, ACTIVE, BS>(ring, f, p, c + 3, acc);
-              }
-              if (c < p.nc) {
-                prefill_step_light<F, 3, NT, ACTIVE, BS>(ring, f, p, c, acc);
-                if (c + 1 < p.nc) {
-                  prefill_step_light<F, 0, NT, ACTIVE, BS>(ring, f, p, c + 1, acc);
-                  if (c + 2 < p.nc) prefill_step_light<F, 1, NT, ACTIVE, BS>(ring, f, p, c + 2, acc);
-                }
-              }
-            }
-          }
-        }
-      }
-    }
-  }
+  // Steps 0 .. kLLead - 1 have their own barrier counts (every path issues the loads in the
+  // order the counts assume), then blocks of kLSlots steps with the steady count.
+  constexpr int BS = B0 + kLLead * L;
+  auto steady = [&]() {
+    int c = kLLead;
+    for (; c + kLSlots <= p.nc; c += kLSlots)
+      prefill_light_block<F, NT, ACTIVE, kLLead, BS>(ring, f, p, c, acc,
+                                                     std::make_integer_sequence<int, kLSlots>());
+    prefill_light_tail<F, NT, ACTIVE, kLLead, BS, 0, 0, kLSlots - 1>(ring, f, p, c, acc,
+                                                                     [] {});
+  };
+  prefill_light_tail<F, NT, ACTIVE, 0, B0, L, 0, kLLead>(ring, f, p, 0, acc, steady);
   // As in prefill_loop: every load has landed before the wave goes on, and the ring's
   // registers are operands of the final wait.
   if constexpr (ACTIVE) {
