@@ -81,6 +81,7 @@ struct PrefillArgs {
                           // expert 0)
   int E;                  // experts: a tile whose expert lies outside [0, E) computes nothing
   int a_by_slot;          // gate_up reads row `slot` of a (pre-scaled rows), not the token's
+  int32_t* inv;           // gate_up, N-tile 0: inv[token * E + expert] = slot (null: none)
   ExpertParams p;
 };
 
@@ -760,6 +761,8 @@ __global__ void __launch_bounds__(kPThreads)
     const uint32_t arow = (GATE_UP && !args.a_by_slot) ? (uint32_t)(tk >= 0 ? tk : 0)
                                                        : (uint32_t)(tk >= 0 ? m0 + tid : m0);
     s_rowoff[tid] = arow * (uint32_t)args.K * 2u;
+    // The combine's slot of each (token, expert) pair, written once per M-tile.
+    if (GATE_UP && args.inv && nt == 0 && tk >= 0) args.inv[(size_t)tk * args.E + e] = m0 + tid;
     const unsigned long long real = __ballot(tk >= 0);
     if (lane == 0) s_lastw[wave] = real ? 64 * wave + 63 - __builtin_clzll(real) : -1;
   }
@@ -925,16 +928,17 @@ __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
 }
 
 // inv[t, e] = slot of (t, e) or -1.
-__global__ void cte_inverse_kernel(const int32_t* __restrict__ tp2id,
-                                   const int32_t* __restrict__ b2e, int64_t n_slots, int B, int T,
-                                   int E, int32_t* __restrict__ inv) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= n_slots) return;
-  const int tk = tp2id[p];
-  if (tk < 0 || tk >= T) return;
-  const int e = b2e[p / B];
-  if (e < 0 || e >= E) return;
-  inv[(size_t)tk * E + e] = (int32_t)p;
+// The slot of (token t, expert e), or -1: inv[t * E + e] as the gate_up GEMM wrote it for
+// the routed pairs, checked against the mapping (slot in range, its token t and its
+// block's expert e), so that stale entries of unrouted pairs count as none and inv needs
+// no clearing before a call.
+__device__ __forceinline__ int cte_slot_of(const int32_t* __restrict__ inv,
+                                           const int32_t* __restrict__ tp2id,
+                                           const int32_t* __restrict__ b2e, int64_t n_slots, int B,
+                                           int t, int e, int E) {
+  const int s = inv[(size_t)t * E + e];
+  if (s < 0 || (int64_t)s >= n_slots) return -1;
+  return (tp2id[s] == t && b2e[s / B] == e) ? s : -1;
 }
 
 // out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.  One
@@ -945,6 +949,7 @@ constexpr int kCombineThreads = 256;
 constexpr int kCteMaxE = 1024;
 __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
+    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int64_t n_slots, int B,
     const float* __restrict__ aff, int H, int E, int scale_mode, int out_f32,
     void* __restrict__ out) {
   constexpr int kWaves = kCombineThreads / 64;
@@ -960,7 +965,7 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
 #pragma unroll
   for (int j = 0; j < kMaxChunks / kWaves; ++j) {
     const int e = (wave + kWaves * j) * 64 + lane;
-    slot[j] = e < E ? inv[(size_t)t * E + e] : -1;
+    slot[j] = e < E ? cte_slot_of(inv, tp2id, b2e, n_slots, B, t, e, E) : -1;
     m[j] = __ballot(slot[j] >= 0);
     if (lane == 0 && wave + kWaves * j < nch) s_cc[wave + kWaves * j] = __popcll(m[j]);
   }
@@ -1054,13 +1059,14 @@ __global__ void __launch_bounds__(256) cte_scale_h_kernel(
 // Grid (T, column chunks of 2048); 8 columns per thread.
 __global__ void __launch_bounds__(256) cte_combine_dense_bf16_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
+    const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int64_t n_slots, int B,
     const uint16_t* __restrict__ expert_const, int H, int E, int out_f32, void* __restrict__ out) {
   const int t = blockIdx.x;
   const int n = blockIdx.y * 2048 + threadIdx.x * 8;
   if (n >= H) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int e = 0; e < E; ++e) {
-    const int slot = inv[(size_t)t * E + e];
+    const int slot = cte_slot_of(inv, tp2id, b2e, n_slots, B, t, e, E);
     const uint16_t* src = slot >= 0 ? y + (size_t)slot * H
                                     : (expert_const ? expert_const + (size_t)e * H : nullptr);
     if (!src) continue;
@@ -1078,11 +1084,6 @@ __global__ void __launch_bounds__(256) cte_combine_dense_bf16_kernel(
     for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(acc[i]);
     *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(out) + (size_t)t * H + n) = r;
   }
-}
-
-__global__ void fill_i32_k(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 struct CteWs {
@@ -1195,6 +1196,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.order = w.order;
   a.E = (int)E;
   a.a_by_slot = pre ? 1 : 0;
+  a.inv = w.inv;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
@@ -1227,6 +1229,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   // down: A = h (K = I), rows = H
   a.a = w.h;
   a.a_by_slot = 0;
+  a.inv = nullptr;
   a.wq = dn_q;
   a.ws = dn_s;
   a.bias = dn_bias;
@@ -1236,18 +1239,15 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.n_ntiles = prefill_ntiles(H, weight_fmt);
   launch_prefill_gemm(false, weight_fmt, a, s);
   mark(2);
-  hipLaunchKernelGGL(fill_i32_k, dim3((unsigned)((T * E + 255) / 256)), dim3(256), 0, s, w.inv,
-                     T * E, -1);
-  hipLaunchKernelGGL(cte_inverse_kernel, dim3((unsigned)((n_slots + 255) / 256)), dim3(256), 0, s,
-                     token_position_to_id, block_to_expert, n_slots, (int)block_size, (int)T,
-                     (int)E, w.inv);
   if (pre || delayed)
     hipLaunchKernelGGL(cte_combine_dense_bf16_kernel,
                        dim3((unsigned)T, (unsigned)((H + 2047) / 2048)), dim3(256), 0, s, w.y,
-                       w.inv, expert_const, (int)H, (int)E, out_f32, out);
+                       w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
+                       expert_const, (int)H, (int)E, out_f32, out);
   else
     hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, s, w.y,
-                       w.inv, affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
+                       w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
+                       affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
   mark(3);
   return check_launch("moe_cte");
 }
