@@ -941,54 +941,49 @@ __device__ __forceinline__ int cte_slot_of(const int32_t* __restrict__ inv,
   return (tp2id[s] == t && b2e[s / B] == e) ? s : -1;
 }
 
-// out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.  One
-// workgroup per token: the token's (slot, weight) pairs are compacted in ascending
-// expert order from its row of inv (a ballot per 64 experts), then each thread sums
-// its 8-column groups over that list.
+// out[t, n] = bf16(sum_e float(y[inv[t,e], n]) * aff[t*E + e]) for e ascending.  One wave
+// per token, four tokens per workgroup: the wave compacts the token's (slot, weight) pairs
+// in ascending expert order from its row of inv (a ballot per 64 experts) into its own
+// LDS list, then each lane sums its 8-column groups over that list.  All of a
+// workgroup's tokens are in flight at once (one round of workgroups on the chip at 4096
+// tokens), so the dependent loads (inv, mapping, weights, rows of y) overlap.
 constexpr int kCombineThreads = 256;
+constexpr int kCombineTok = kCombineThreads / 64;
 constexpr int kCteMaxE = 1024;
 __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
     const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int64_t n_slots, int B,
-    const float* __restrict__ aff, int H, int E, int scale_mode, int out_f32,
+    const float* __restrict__ aff, int T, int H, int E, int scale_mode, int out_f32,
     void* __restrict__ out) {
-  constexpr int kWaves = kCombineThreads / 64;
-  constexpr int kMaxChunks = kCteMaxE / 64;
-  __shared__ int s_slot[kCteMaxE];
-  __shared__ float s_w[kCteMaxE];
-  __shared__ int s_cc[kMaxChunks];
-  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nch = (E + 63) / 64;
+  __shared__ int s_slot[kCombineTok][kCteMaxE];
+  __shared__ float s_w[kCombineTok][kCteMaxE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * kCombineTok + wave;
+  const bool live = t < T;
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int slot[kMaxChunks / kWaves];
-  unsigned long long m[kMaxChunks / kWaves];
-#pragma unroll
-  for (int j = 0; j < kMaxChunks / kWaves; ++j) {
-    const int e = (wave + kWaves * j) * 64 + lane;
-    slot[j] = e < E ? cte_slot_of(inv, tp2id, b2e, n_slots, B, t, e, E) : -1;
-    m[j] = __ballot(slot[j] >= 0);
-    if (lane == 0 && wave + kWaves * j < nch) s_cc[wave + kWaves * j] = __popcll(m[j]);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kMaxChunks / kWaves; ++j) {
-    if (slot[j] < 0) continue;
-    const int ch = wave + kWaves * j, e = ch * 64 + lane;
-    int pos = __popcll(m[j] & below);
-    for (int k = 0; k < ch; ++k) pos += s_cc[k];
-    s_slot[pos] = slot[j];
-    s_w[pos] = scale_mode == MXMOE_SCALE_NO ? 1.0f : aff[(size_t)t * E + e];
-  }
   int cnt = 0;
-  for (int k = 0; k < nch; ++k) cnt += s_cc[k];
+  if (live) {
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int sl = e < E ? cte_slot_of(inv, tp2id, b2e, n_slots, B, t, e, E) : -1;
+      const unsigned long long m = __ballot(sl >= 0);
+      if (sl >= 0) {
+        const int pos = cnt + __popcll(m & below);
+        s_slot[wave][pos] = sl;
+        s_w[wave][pos] = scale_mode == MXMOE_SCALE_NO ? 1.0f : aff[(size_t)t * E + e];
+      }
+      cnt += __popcll(m);
+    }
+  }
   __syncthreads();
+  if (!live) return;
   typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-  for (int n = tid * 8; n < H; n += kCombineThreads * 8) {
+  for (int n = lane * 8; n < H; n += 64 * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
     for (int k = 0; k < cnt; ++k) {
-      const float a = s_w[k];
-      const u16x8 v = *reinterpret_cast<const u16x8*>(y + (size_t)s_slot[k] * H + n);
+      const float a = s_w[wave][k];
+      const u16x8 v = *reinterpret_cast<const u16x8*>(y + (size_t)s_slot[wave][k] * H + n);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
     }
@@ -1245,9 +1240,10 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                        w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
                        expert_const, (int)H, (int)E, out_f32, out);
   else
-    hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)T), dim3(kCombineThreads), 0, s, w.y,
-                       w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
-                       affinities_masked, (int)H, (int)E, scale_mode, out_f32, out);
+    hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
+                       dim3(kCombineThreads), 0, s, w.y, w.inv, token_position_to_id,
+                       block_to_expert, n_slots, (int)block_size, affinities_masked, (int)T,
+                       (int)H, (int)E, scale_mode, out_f32, out);
   mark(3);
   return check_launch("moe_cte");
 }
