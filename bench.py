@@ -14,7 +14,7 @@ that the steps rotate through, so a step never finds its weights in the 256 MB
 last-level cache.  Inputs are resident in HBM before timing starts.
 
 Per-kernel durations come from HIP events the library records on the launch stream
-around each stage of every timed step.  ``roofline`` covers the dominant kernel of
+around each stage, in an eager pass of their own; the timed regions record none.  ``roofline`` covers the dominant kernel of
 the headline step (decode gate_up weight streaming: HBM bound); ``prefill.roofline``
 covers the prefill gate_up GEMM (MFMA bound, bf16 MFMA after in-register dequant).
 
@@ -159,8 +159,18 @@ def cpu_baseline(wl, decode_T, prefill_T):
     from oracle.layer import RefLayer
 
     E, K, H, I, limit, biases, _, _ = WORKLOADS[wl]
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    # The process's affinity cores, at most 16: the host share one GPU's jobs get on a
+    # node of 8 GPUs, whatever the affinity mask shows.
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, 16)
     torch.set_num_threads(cores)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                         "unknown")
+    except OSError:
+        pass
     e_s = min(E, 16)
     shape = synthetic.MoEShape(wl + "-sample", E, min(K, e_s), H, I, limit, biases)
     ref = RefLayer(synthetic.layer_tensors(shape, 5, E=e_s))
@@ -179,6 +189,7 @@ def cpu_baseline(wl, decode_T, prefill_T):
     t, n = timed(lambda: ref.decode(x), 8.0)
     t *= E / e_s
     res["decode"] = {"value": decode_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+                     "cpu": model, "affinity_cores": affinity,
                      "sample": f"dense all-expert fp32 decode (reference moe_block_tkg CPU flow) "
                                f"of {decode_T} tokens over {e_s} of {E} experts, median of {n} "
                                f"reps (about 8 s), time scaled x{E / e_s:g} (linear in experts)"}
@@ -187,6 +198,7 @@ def cpu_baseline(wl, decode_T, prefill_T):
     t, n = timed(lambda: ref.prefill(xp), 8.0)
     t *= (E / e_s) * (prefill_T / t_s)
     res["prefill"] = {"value": prefill_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+                      "cpu": model, "affinity_cores": affinity,
                       "sample": f"dense all-expert bf16 prefill (reference _torch_moe_impl CPU "
                                 f"flow) of {t_s} tokens over {e_s} of {E} experts, median of {n} "
                                 f"reps (about 8 s), time scaled x{E / e_s:g} (experts) "
@@ -340,17 +352,23 @@ def main():
         torch.cuda.synchronize()
         p_settled = settle(lambda n: (layers[n % L].prefill(xp[n % L]), 1)[1], args.settle)
         ps = args.prefill_steps
+        # Per-kernel durations from a pass with the library's stage events; the timed
+        # region below records none (each event recorded between two kernels of the step
+        # delays the next one by a few microseconds).
         pst = [[ev() for _ in range(4)] for _ in range(ps)]
-        p0, p1 = ev(), ev()
-        p0.record()
         for s in range(ps):
             layers[s % L].prefill(xp[s % L], stage_events=pst[s])
-        p1.record()
         torch.cuda.synchronize()
-        pms = p0.elapsed_time(p1) / ps
         gu_ms_p = sum(pst[s][0].elapsed_time(pst[s][1]) for s in range(ps)) / ps
         dn_ms_p = sum(pst[s][1].elapsed_time(pst[s][2]) for s in range(ps)) / ps
         cb_ms_p = sum(pst[s][2].elapsed_time(pst[s][3]) for s in range(ps)) / ps
+        p0, p1 = ev(), ev()
+        p0.record()
+        for s in range(ps):
+            layers[s % L].prefill(xp[s % L])
+        p1.record()
+        torch.cuda.synchronize()
+        pms = p0.elapsed_time(p1) / ps
         pairs = pT * K
         flops = 6 * H * I * pairs + 2 * pT * H * E
         gu_flops = 4 * H * I * pairs
