@@ -101,7 +101,10 @@ __device__ __forceinline__ void tkg_route_block(
     off[tid] = v - cnt;
     expert_off[tid] = v - cnt;
     if (cnt > 0) active[a - 1] = tid;
-    for (int j = 0; j < ntl; ++j) tiles[tl - ntl + j] = (tid << 16) | j;
+    // (expert, first slot, tokens) per 16-token tile: one load gives an item all it needs
+    for (int j = 0; j < ntl; ++j)
+      reinterpret_cast<int4*>(tiles)[tl - ntl + j] =
+          make_int4(tid, v - cnt + 16 * j, min(16, cnt - 16 * j), 0);
   }
   if (tid == E - 1) {
     expert_off[E] = v;
@@ -468,7 +471,8 @@ struct TkgArgs {
   const int32_t* active;
   const int32_t* n_active;
   const int32_t* slot_tok;
-  const int32_t* tiles;    // (expert << 16 | tile) of the routed batch, and their count
+  const int32_t* tiles;    // (expert, first slot, tokens, 0) per 16-token tile of the routed
+                           // batch, and their count
   const int32_t* n_tiles;
   uint16_t* out_hi;        // gate_up: h (hi, lo)
   uint16_t* out_lo;
@@ -504,25 +508,25 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
   // Item metadata is wave-uniform: keep it in scalar registers.  With one token tile per
   // pass (NT = 1) an item is (token tile, row groups): an expert's 16-token tiles are
   // separate items; else (active expert, row groups), looping over the expert's tokens.
-  int e, tb_first = 0;
+  int e, s0, ne;
   if constexpr (NT == 1) {
-    const int tile = __builtin_amdgcn_readfirstlane(a.tiles[ai]);
-    e = tile >> 16;
-    tb_first = (tile & 0xffff) * 16;
+    const int4 tm = reinterpret_cast<const int4*>(a.tiles)[ai];
+    e = __builtin_amdgcn_readfirstlane(tm.x);
+    s0 = __builtin_amdgcn_readfirstlane(tm.y);
+    ne = __builtin_amdgcn_readfirstlane(tm.z);
   } else {
     e = __builtin_amdgcn_readfirstlane(a.active[ai]);
+    s0 = __builtin_amdgcn_readfirstlane(a.expert_off[e]);
+    ne = __builtin_amdgcn_readfirstlane(a.expert_off[e + 1]) - s0;
   }
   const int rg0 = ri * R;
   g.wq = a.wq + ((size_t)e * n_rg + rg0) * (size_t)g.rg_bytes;
   g.ws = a.ws + ((size_t)e * ((n_rg + 3) / 4) + rg0 / 4) * (size_t)(2 * K);
   g.rv = min(R, n_rg - rg0);
-  const int s0 = __builtin_amdgcn_readfirstlane(a.expert_off[e]);
-  const int ne = __builtin_amdgcn_readfirstlane(a.expert_off[e + 1]) - s0;
   const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
                            : reinterpret_cast<const char*>(a.h_hi);
   const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
-  const int tb_end = NT == 1 ? min(ne, tb_first + 16) : ne;
-  for (int tb = tb_first; tb < tb_end; tb += 16 * NT) {
+  for (int tb = 0; tb < ne; tb += 16 * NT) {
     uint32_t row_off[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -751,7 +755,7 @@ static size_t tkg_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I,
   t.slot_tok = cv.take<int32_t>(S);
   t.tok_slot = cv.take<int32_t>(S);
   t.tok_w = cv.take<float>(S);
-  t.tiles = cv.take<int32_t>(tkg_max_tiles(T, E, K));
+  t.tiles = cv.take<int32_t>(4 * tkg_max_tiles(T, E, K));
   t.n_tiles = cv.take<int32_t>(1);
   t.h_hi = cv.take<uint16_t>(S * I);
   t.h_lo = cv.take<uint16_t>(S * I);
