@@ -475,6 +475,10 @@ __device__ __forceinline__ void prefill_loop(const Stage& stage, const PrefillTi
 // chunks ahead.  Wave w brings rows 4 (w + 4j) .. 4 (w + 4j) + 3, j < NT.
 constexpr int kLLead = 7, kLStages = 8, kLSlots = 8;
 static_assert(kLStages > kLLead && (kLStages & (kLStages - 1)) == 0, "light ring");
+// The light loop's direct loads give wave w rows 4 (w + 4 j) of subtile j: exactly the
+// 16 NT rows of a ring slice with 4 waves.  Any other wave count writes past the slice
+// (and past the workgroup's LDS in the last slice of a 2-subtile ring).
+static_assert(kPWaves == 4, "the light loop maps each 16-row subtile onto 4 waves");
 
 template <int NT>
 __device__ __forceinline__ void prefill_rowoffs_light(const PrefillTile& p, uint32_t (&ro)[NT]) {
