@@ -18,6 +18,13 @@ class ActFnType(Enum):
     Swish = "Swish"
 
 
+class NormType(Enum):
+    NO_NORM = "NO_NORM"
+    RMS_NORM = "RMS_NORM"
+    RMS_NORM_SKIP_GAMMA = "RMS_NORM_SKIP_GAMMA"
+    LAYER_NORM = "LAYER_NORM"
+
+
 class ExpertAffinityScaleMode(Enum):
     NO_SCALE = "NO_SCALE"
     POST_SCALE = "POST_SCALE"

@@ -200,6 +200,28 @@ def interleave_row_groups(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return torch.cat([g, u], 2).reshape(E, 2 * I, *rest)
 
 
+def fuse_gate_up(gate_q: torch.Tensor, gate_s: torch.Tensor, up_q: torch.Tensor,
+                 up_s: torch.Tensor):
+    """Packed gate and up projections of one MLP (MXFP4 or MXFP8, each data [I/16, bytes]
+    and scale [ceil(I/64), 2K]) -> the fused gate_up of an expert: data [2I/16, bytes] with
+    gate and up 16-row groups alternating, scale [ceil(2I/64), 2K].  The data of a row group
+    is self-contained, so the rows interleave as they are; scales are packed four row
+    groups to a quad and are re-packed."""
+    if gate_q.shape != up_q.shape or gate_s.shape != up_s.shape or gate_q.dim() != 2:
+        raise ValueError(f"gate {tuple(gate_q.shape)}/{tuple(gate_s.shape)} and up "
+                         f"{tuple(up_q.shape)}/{tuple(up_s.shape)} must be equal 2-D packed "
+                         "tensors")
+    nrg = gate_q.shape[0]
+    G = gate_s.shape[1] // 64
+    if gate_s.shape != ((nrg * 16 + 63) // 64, 64 * G):
+        raise ValueError(f"scale shape {tuple(gate_s.shape)} does not match {nrg} row groups")
+    data = torch.stack([gate_q, up_q], 1).reshape(2 * nrg, gate_q.shape[1]).contiguous()
+    sg = _unpack_scales(gate_s, nrg * 16, G)
+    su = _unpack_scales(up_s, nrg * 16, G)
+    sc = interleave_row_groups(sg, su)  # [1, 2I, G]
+    return data, _pack_scales(sc)[0]
+
+
 def deinterleave_rows(t: torch.Tensor):
     """Checkpoint gate_up rows (2i = gate_i, 2i+1 = up_i) -> (gate, up) along dim 1."""
     return t[:, 0::2], t[:, 1::2]
