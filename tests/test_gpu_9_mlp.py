@@ -83,14 +83,53 @@ def test_mlp_mx_weights_cached_and_updated(dev):
     a = run()
     check_close(a, om.torch_mlp_impl(x, gd.T.contiguous(), ud.T.contiguous(),
                                      dd.T.contiguous()).float(), label="mlp before update")
-    (uq2, _), ud2 = _weights("mxfp4", 79, I, H)
-    # same scales, new codes: the dense reference needs the codes dequantized with us
+    # new codes under the same scales: the dense reference dequantizes them with up's scales
     from vllm_neuron_amd.weights import unpack_mxfp4
-    b2, _ = unpack_mxfp4(uq2, us)
-    _, s_up = unpack_mxfp4(uq, us)
+    (uq2, _), _ = _weights("mxfp4", 79, I, H)
+    b2, s_up = unpack_mxfp4(uq2, us)
     ud2 = o4.dequantize_mxfp4_to_bf16(b2, s_up).reshape(I, H)
     uq_d.copy_(uq2.to(dev))
     b = run()
     check_close(b, om.torch_mlp_impl(x, gd.T.contiguous(), ud2.T.contiguous(),
                                      dd.T.contiguous()).float(), label="mlp after update")
     assert not torch.equal(a, b)
+
+
+def test_mlp_mx_graph_replays(dev):
+    """The dense MLP (mapping, tile order, both GEMMs, combine) captured in a HIP graph after
+    one eager call: every replay, with eager work and synchronizations between them, equals
+    the eager result for its input."""
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.enums import QuantizationType
+    from vllm_neuron_amd.functional import mlp
+
+    T, H, I = 200, 512, 384
+    (gq, gs), _ = _weights("mxfp4", 83, I, H)
+    (uq, us), _ = _weights("mxfp4", 89, I, H)
+    (dq, ds), _ = _weights("mxfp4", 97, H, I)
+    w = [t.to(dev) for t in (gq, uq, dq, gs, us, ds)]
+    gb = synthetic.normal_bf16(101, (1, I), 0.1).to(dev)
+    run = lambda xx: mlp(xx, w[0], w[1], w[2], quantization_type=QuantizationType.MX,  # noqa: E731
+                         gate_w_scale=w[3], up_w_scale=w[4], down_w_scale=w[5], gate_b=gb)
+    xs = [synthetic.normal_bf16(103 + i, (T, H)).to(dev) for i in range(3)]
+    eager = [run(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(static_x)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out = run(static_x)
+    for rep in range(2):
+        for i, x in enumerate(xs):
+            static_x.copy_(x)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager[i]), (rep, i)
+            other = run(xs[(i + 1) % 3])  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(other, eager[(i + 1) % 3])

@@ -100,9 +100,11 @@ def _identity_mapping(T: int, dev: torch.device):
         aff_m, tp2id, b2e, _ = build_blockwise_mapping(ones, 1, 1, _BLOCK)
         hit = (aff_m.reshape(-1).contiguous(), tp2id.contiguous(), b2e.contiguous(),
                b2e.numel())
-        if len(_MAPPINGS) >= 16:
-            _MAPPINGS.clear()
-        _MAPPINGS[key] = hit
+        # Tensors made during a graph capture live in the graph's pool: not kept.
+        if not torch.cuda.is_current_stream_capturing():
+            if len(_MAPPINGS) >= 16:
+                _MAPPINGS.clear()
+            _MAPPINGS[key] = hit
     return hit
 
 
