@@ -27,6 +27,9 @@ CASES = [
     (4096, 32, 4, 256, None), (4096, 32, 4, 256, 1.2), (4096, 128, 4, 256, None),
     (8192, 256, 8, 256, 1.0), (300, 7, 3, 128, None), (257, 1, 1, 128, None),
     (1000, 16, 16, 128, None), (16384, 64, 2, 512, 2.0),
+    # the largest expert count the kernels take (1,024), and a large one that is not a
+    # multiple of 4 (affinity rows read one element at a time)
+    (96, 1024, 8, 128, None), (130, 1001, 8, 256, 1.0),
 ]
 
 
