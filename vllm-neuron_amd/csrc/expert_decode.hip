@@ -696,14 +696,18 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // Work split of a decode batch of the one-tile kernels.  A batch touching few experts has
 // fewer row-group items than wave slots and is latency-bound (each wave streams one item
 // with one or two chunks in flight).  Such batches split each item's K into parts, each
-// part its own work unit: gate_up in 2 parts when it has under 1,000 items (the raw part
+// part its own work unit: gate_up in 2 parts when it has under 2,000 items (the raw part
 // sums go through the activation kernel), the down projection of 4-row-group items into
-// parts of about 400 items in all (at most 8; the first part adds the bias and the
-// combine adds the parts in order).  Measured on the 20B-shaped layer: 1 token
-// 47.4 -> 37.5 us per step, 4 tokens about 5 % faster, 16 and more tokens unchanged (a
-// part costs a unit start-up and a combine read, which larger batches do not win back).
-constexpr double kTkgGateUpSplitItems = 1000.0;
-constexpr double kTkgDownSplitTarget = 400.0;
+// parts of about 1,500 units in all (at most 3; the first part adds the bias and the
+// combine adds the parts in order).  Measured on the 20B-shaped layer, us per step: 1 token
+// 47.4 unsplit -> 37.5; against the earlier thresholds (1,000 items; 400 units, at most 8)
+// on one box, 4 tokens 64.6 -> 61.2, 16 tokens 99.3 -> 95.6, 1 and 64 tokens unchanged (the
+// 64-token down items are the wide ones).  More parts lose: each costs a unit
+// start-up and a combine read (8 down parts at 1 token: +7 us), and so does a gate_up
+// split at 2,700 items and more (16 tokens: +0.5 us; 64 tokens: +16 us).
+constexpr double kTkgGateUpSplitItems = 2000.0;
+constexpr double kTkgDownSplitTarget = 1500.0;
+constexpr int kTkgDownMaxParts = 3;
 struct TkgSplit {
   int nq_gu = 1, nq_dn = 1;    // K parts
   int cpq_gu = 1 << 20, cpq_dn = 1 << 20;  // 128-wide chunks per part
@@ -731,7 +735,8 @@ static TkgSplit tkg_split(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
   if (sp.dn_wide) return sp;
   const double dn_items = tiles * (double)((H / 16 + 3) / 4);
   const int want = (int)ceil(kTkgDownSplitTarget / (dn_items > 1.0 ? dn_items : 1.0));
-  tkg_parts((int)((I + 127) / 128), want < 1 ? 1 : (want > 8 ? 8 : want), sp.nq_dn, sp.cpq_dn);
+  tkg_parts((int)((I + 127) / 128), want < 1 ? 1 : (want > kTkgDownMaxParts ? kTkgDownMaxParts : want),
+            sp.nq_dn, sp.cpq_dn);
   return sp;
 }
 
