@@ -15,7 +15,7 @@ def gptoss20(dev):
     return build(synthetic.GPT_OSS_20B, 1, dev)
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 64])
+@pytest.mark.parametrize("T", [1, 4, 16, 48, 64])
 def test_decode_gptoss20b(dev, gptoss20, T):
     from vllm_neuron_amd import synthetic
 

@@ -705,9 +705,16 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // 64-token down items are the wide ones).  More parts lose: each costs a unit
 // start-up and a combine read (8 down parts at 1 token: +7 us), and so does a gate_up
 // split at 2,700 items and more (16 tokens: +0.5 us; 64 tokens: +16 us).
+// Wide down items (8 row groups, one-wave workgroups, 12 per CU: 3,072 wave slots on 256
+// CUs) split in 2 parts while both parts of every item still fit one round of slots, i.e.
+// under 1,400 items (margin for the expected tile count): 20B-shaped layer, 48 tokens
+// (~965 items) 110.2 -> 103.5 us, 64 tokens (~1,058) 115.0 -> 109.5; 3 parts at 64 tokens
+// gain nothing; on the 120B-shaped layer, whose 24 to 64-token batches have 1,610 to
+// 2,770 wide items, 2 parts lose 5 to 9 us.
 constexpr double kTkgGateUpSplitItems = 2000.0;
 constexpr double kTkgDownSplitTarget = 1500.0;
 constexpr int kTkgDownMaxParts = 3;
+constexpr double kTkgWideSplitItems = 1400.0;
 struct TkgSplit {
   int nq_gu = 1, nq_dn = 1;    // K parts
   int cpq_gu = 1 << 20, cpq_dn = 1 << 20;  // 128-wide chunks per part
@@ -731,8 +738,12 @@ static TkgSplit tkg_split(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
   const double tiles = active + ((double)(T * K) - active) / 16.0;  // 16-token tiles
   const double gu_items = tiles * (double)((2 * I / 16 + 3) / 4);
   if (gu_items < kTkgGateUpSplitItems) tkg_parts((int)((H + 127) / 128), 2, sp.nq_gu, sp.cpq_gu);
-  sp.dn_wide = tiles * (double)((H / 16 + 7) / 8) >= 900.0;
-  if (sp.dn_wide) return sp;
+  const double wide_items = tiles * (double)((H / 16 + 7) / 8);
+  sp.dn_wide = wide_items >= 900.0;
+  if (sp.dn_wide) {
+    if (wide_items < kTkgWideSplitItems) tkg_parts((int)((I + 127) / 128), 2, sp.nq_dn, sp.cpq_dn);
+    return sp;
+  }
   const double dn_items = tiles * (double)((H / 16 + 3) / 4);
   const int want = (int)ceil(kTkgDownSplitTarget / (dn_items > 1.0 ? dn_items : 1.0));
   tkg_parts((int)((I + 127) / 128), want < 1 ? 1 : (want > kTkgDownMaxParts ? kTkgDownMaxParts : want),
@@ -870,16 +881,17 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     // size), 8 row groups per item with one chunk in flight, three waves per SIMD, one
     // wave per workgroup: a 64-token batch's down items then run in one round, spread
     // over the CUs one wave at a time so that every CU streams about the same share of
-    // the weights.  With few items, 4 row groups and two chunks in flight per wave, each
-    // item's K in nq_dn parts (the first part adds the bias; the combine adds the parts
-    // in order).
+    // the weights (in 2 K parts when both fit that round).  With few items, 4 row groups
+    // and two chunks in flight per wave.  Each item's K in nq_dn parts: the first part adds
+    // the bias, the combine adds the parts in order.
     dn.part_stride = (size_t)S * (size_t)H;
+    dn.nq = sp.nq_dn;
+    dn.cpq = sp.cpq_dn;
     if (sp.dn_wide) {
-      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 1, 1>), grid(false, 8, 1, n_tile_max),
-                         dim3(64), kLds12x1, s, dn);
+      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, false, 1, 1>),
+                         dim3(grid(false, 8, 1, n_tile_max).x * sp.nq_dn), dim3(64), kLds12x1, s,
+                         dn);
     } else {
-      dn.nq = sp.nq_dn;
-      dn.cpq = sp.cpq_dn;
       hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 4>),
                          dim3(grid(false, 4, 4, n_tile_max).x * sp.nq_dn), dim3(256), kLds3x4, s,
                          dn);
