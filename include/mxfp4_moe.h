@@ -66,6 +66,9 @@ extern "C" {
  * (E4M3FN, [rows/16, 16K] bytes); the scales are packed alike ([ceil(rows/64), 2K]). */
 #define MXMOE_WFMT_MXFP4 0
 #define MXMOE_WFMT_MXFP8 1
+/* bf16 expert weights as the reference's shard_on_block takes them (moe_cte.py:117-124):
+ * gate_up [E, H, 2, I] and down [E, I, H], rows along K, no scales (mxmoe_moe_cte only). */
+#define MXMOE_WFMT_BF16 2
 
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -187,6 +190,9 @@ int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* padding_mask
  * x bf16 [>=T, H]; affinities_masked fp32 [T*E]; gu_q/gu_s packed [E][2I x H];
  * dn_q/dn_s packed [E][H x I], both in weight_fmt (MXMOE_WFMT_MXFP4, or MXMOE_WFMT_MXFP8:
  * the MxFP8 weights of the reference's shard_on_block_mx kernel, moe_cte.py:136-138);
+ * with MXMOE_WFMT_BF16, gu_q is bf16 [E, H, 2, I] and dn_q bf16 [E, I, H] (the
+ * shard_on_block operands of the bf16 model, model_bf16.py:1360-1391; 16-byte aligned)
+ * and gu_s / dn_s are ignored (may be NULL);
  * gu_bias bf16 [E, 2, I] or NULL; dn_bias bf16 [E, H] or NULL; out [T, H] in bf16, or
  * fp32 when out_f32 = 1.
  * scale_mode:

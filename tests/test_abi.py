@@ -58,10 +58,20 @@ def test_argument_errors_are_reported():
                            dummy, 4, 100, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
                            None, None)
     assert rc == -1 and b"block_size" in lib.mxmoe_last_error()
-    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, 2, None, None, None, dummy,
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, dummy, dummy, dummy, 3, None, None, None, dummy,
                            dummy, 4, 256, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
                            None, None)
     assert rc == -1 and b"weight format" in lib.mxmoe_last_error()
+    # bf16 weights: no scales needed, rows read 16 bytes at a time
+    odd = ctypes.c_void_p(18)
+    rc = lib.mxmoe_moe_cte(dummy, dummy, odd, None, dummy, None, 2, None, None, None, dummy,
+                           dummy, 4, 256, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
+                           None, None)
+    assert rc == -1 and b"16-byte aligned" in lib.mxmoe_last_error()
+    rc = lib.mxmoe_moe_cte(dummy, dummy, dummy, None, dummy, None, 0, None, None, None, dummy,
+                           dummy, 4, 256, 64, 2880, 2880, 8, 2, None, 0, 0, dummy, dummy, 1 << 30,
+                           None, None)
+    assert rc == -1 and b"null pointer" in lib.mxmoe_last_error()
     rc = lib.mxmoe_linear(dummy, 4, dummy, dummy, 5, 64, 64, dummy, None)
     assert rc == -1 and b"weight format" in lib.mxmoe_last_error()
     rc = lib.mxmoe_dequant_mxfp8_bf16(dummy, dummy, dummy, 4, 48, None)

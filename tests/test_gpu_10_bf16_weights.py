@@ -1,0 +1,205 @@
+"""bf16 expert weights (the reference's shard_on_block operands, the bf16 GPT-OSS model's
+prefill call model_bf16.py:1360-1391) through moe_cte, and the dense mlp with
+quantization NONE, against the oracle's torch flows on the same bf16 weights
+(moe_cte.py:448-581; mlp.py:371-418).  Bounds: normalized max 2e-2, mean 5e-3
+(tests/moe_helpers.check_close)."""
+
+import pytest
+import torch
+
+from moe_helpers import check_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_experts(seed, E, H, I, bias_scale=0.05):
+    """gate_up [E, H, 2I] (gate columns, then up), down [E, I, H], biases [E, 2I] and
+    [E, H]: the bf16 model's parameter shapes (model_bf16.py:1086-1115)."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s, std: (torch.randn(*s, generator=g) * std).to(torch.bfloat16)  # noqa: E731
+    return (r(E, H, 2 * I, std=H ** -0.5), r(E, I, H, std=I ** -0.5),
+            r(E, 2 * I, std=bias_scale), r(E, H, std=bias_scale))
+
+
+def _route(seed, T, E, k):
+    from vllm_neuron_amd import synthetic
+
+    logits = synthetic.normal_bf16(seed, (T, E)).float()
+    top = torch.topk(logits, k, dim=1)
+    return torch.zeros(T, E).scatter_(1, top.indices, torch.softmax(top.values, 1))
+
+
+CASES = [
+    # E, k, H, I, T, block, activation, clamps, biases
+    (8, 2, 256, 512, 300, 256, "Swish", True, True),
+    (6, 2, 416, 288, 77, 128, "SiLU", False, True),    # K and N tails in both GEMMs
+    (4, 1, 96, 64, 129, 512, "GELU", False, False),
+    (3, 3, 128, 96, 1, 128, "Swish", True, True),      # one token
+]
+
+
+@pytest.mark.parametrize("E,k,H,I,T,block,act,clamp,biases", CASES)
+def test_moe_cte_bf16_weights(dev, E, k, H, I, T, block, act, clamp, biases):
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.enums import MoECTEImplementation
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    print(f"moe_cte bf16 E={E} k={k} H={H} I={I} T={T} block={block} {act}", flush=True)
+    gu, dn, gb, db = _bf16_experts(80 + H + I, E, H, I)
+    x = synthetic.tokens(81, T, H)
+    aff = _route(82 + T, T, E, k)
+    lim = dict(gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+               up_clamp_lower_limit=-6.0) if clamp else {}
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), E, k, block)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    got = NF.moe_cte(implementation=MoECTEImplementation.shard_on_block, conditions=cond,
+                     hidden_states=x.to(dev), expert_affinities_masked=am_g,
+                     gate_up_proj_weight=mv(gu).reshape(E, H, 2, I), down_proj_weight=mv(dn),
+                     gate_and_up_proj_bias=mv(gb).reshape(E, 2, I) if biases else None,
+                     down_proj_bias=mv(db).unsqueeze(1) if biases else None,
+                     activation_function=act, block_size=block, token_position_to_id=tp,
+                     block_to_expert=b2e, expert_affinities_scaling_mode="POST_SCALE",
+                     skip_token=True, is_tensor_update_accumulating=True, **lim).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, E, k, block)
+    want = oc.torch_moe_impl(x, am_r, gu.reshape(E, H, 2, I), dn,
+                             gb.reshape(E, 2, I) if biases else None,
+                             db.unsqueeze(1) if biases else None, activation_function=act, **lim)
+    assert got.dtype == torch.bfloat16
+    check_close(got.float(), want.float(), None, f"moe_cte bf16 E={E} H={H} I={I} T={T}")
+
+
+def test_moe_cte_bf16_weights_gptoss20b_shape(dev):
+    """20B-shaped layer (E=32, top-4, H = I = 2880, clamped Swish) at 2,048 tokens: the
+    partial last K chunk (2880 = 22.5 x 128) and down N-tile; sampled rows through the
+    routed form of the same flow."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    E, k, H, I, T = 32, 4, 2880, 2880, 2048
+    gu, dn, gb, db = _bf16_experts(90, E, H, I)
+    x = synthetic.tokens(91, T, H)
+    aff = _route(92, T, E, k)
+    lim = dict(gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), E, k, 256)
+    got = NF.moe_cte(x.to(dev), am_g, gu.to(dev).reshape(E, H, 2, I), dn.to(dev), tp, b2e, 256,
+                     implementation="shard_on_block", gate_and_up_proj_bias=gb.to(dev),
+                     down_proj_bias=db.to(dev), activation_function="Swish", **lim).cpu()
+    rows = torch.arange(0, T, 37)
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff, E, k, 256)
+    want = oc.torch_moe_impl_routed(x, am_r, gu.reshape(E, H, 2, I), dn, gb.reshape(E, 2, I),
+                                    db.unsqueeze(1), activation_function="Swish",
+                                    token_rows=rows, **lim)
+    check_close(got[rows].float(), want, None, "moe_cte bf16 20b shape")
+
+
+@pytest.mark.parametrize("mode", ["PRE_SCALE", "PRE_SCALE_DELAYED"])
+def test_moe_cte_bf16_weights_prescale_modes(dev, mode):
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+
+    E, k, H, I, T = 8, 2, 256, 384, 200
+    gu, dn, gb, db = _bf16_experts(95, E, H, I, bias_scale=1.0)
+    x = synthetic.tokens(96, T, H)
+    aff16 = _route(97, T, E, k).to(torch.bfloat16)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff16.float().to(dev), E, k, 256)
+    got = NF.moe_cte(x.to(dev), am_g, gu.to(dev).reshape(E, H, 2, I), dn.to(dev), tp, b2e, 256,
+                     implementation="shard_on_block", gate_and_up_proj_bias=gb.to(dev),
+                     down_proj_bias=db.to(dev), activation_function="Swish",
+                     expert_affinities_scaling_mode=mode, gate_clamp_upper_limit=7.0).cpu()
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff16.float(), E, k, 256)
+    want = oc.torch_moe_impl(x, am_r.to(torch.bfloat16), gu.reshape(E, H, 2, I), dn,
+                             gb.reshape(E, 2, I), db.unsqueeze(1), gate_clamp_upper_limit=7.0,
+                             activation_function="Swish", expert_affinities_scaling_mode=mode)
+    check_close(got.float(), want.float(), None, f"moe_cte bf16 {mode}")
+
+
+def test_bf16_model_prefill_call_chain(dev):
+    """The bf16 GPT-OSS model's prefill MoE (model_bf16.py:1282-1391) with its argument
+    lists: router (fp32 softmax routing) -> build_blockwise_mapping -> moe_cte
+    (shard_on_block, reshaped [E, H, 2I] parameters, [E, 2I] / [E, H] biases) against the
+    oracle's router, mapping and moe_cte torch flows."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.enums import ExpertAffinityScaleMode, MoECTEImplementation
+
+    from oracle import blockwise as ob
+    from oracle import moe_cte as oc
+    from oracle import router as orr
+
+    E, k, H, I, T, block, limit = 16, 4, 512, 384, 333, 256, 7.0
+    gu, dn, gb, db = _bf16_experts(98, E, H, I)
+    x = synthetic.tokens(99, T, H)
+    rw = synthetic.normal_bf16(100, (E, H), 0.02)
+    rb = synthetic.normal_bf16(101, (E,), 0.02)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    aff = NF.router(hidden_states=x.to(dev), router_weights=mv(rw).T, top_k=k,
+                    router_bias=mv(rb), activation="softmax", computation_dtype=torch.float32)
+    am, tp, b2e, cond = NF.build_blockwise_mapping(expert_affinities=aff, num_local_experts=E,
+                                                   num_experts_per_token=k, block_size=block)
+    got = NF.moe_cte(
+        implementation=MoECTEImplementation.shard_on_block, conditions=cond,
+        hidden_states=x.to(dev), expert_affinities_masked=am,
+        gate_up_proj_weight=mv(gu).reshape(E, H, 2, I), down_proj_weight=mv(dn),
+        gate_and_up_proj_bias=mv(gb).reshape(E, 2, I), down_proj_bias=mv(db).unsqueeze(1),
+        activation_function="Swish", block_size=block,
+        token_position_to_id=tp.to(dtype=torch.int32), block_to_expert=b2e.to(dtype=torch.int32),
+        expert_affinities_scaling_mode=ExpertAffinityScaleMode.POST_SCALE, skip_token=True,
+        gate_clamp_upper_limit=limit, gate_clamp_lower_limit=None,
+        up_clamp_upper_limit=limit + 1, up_clamp_lower_limit=-limit + 1,
+        is_tensor_update_accumulating=True, compute_dtype="bfloat16").cpu()
+    aff_r = orr.router(x, rw.T, k, rb, "softmax", computation_dtype=torch.float32)
+    assert torch.equal(aff.cpu() != 0, aff_r != 0), "selected experts differ"
+    am_r, _, _, _ = ob.build_blockwise_mapping(aff_r, E, k, block)
+    want = oc.torch_moe_impl(x, am_r, gu.reshape(E, H, 2, I), dn, gb.reshape(E, 2, I),
+                             db.unsqueeze(1), gate_clamp_upper_limit=limit,
+                             up_clamp_upper_limit=limit + 1, up_clamp_lower_limit=-limit + 1,
+                             activation_function="Swish")
+    check_close(got.float(), want.float(), None, "bf16 model prefill chain")
+
+
+@pytest.mark.parametrize("T,H,I,act,bias", [(1, 256, 384, "SiLU", True), (200, 416, 288, "GELU", False),
+                                            (1000, 2880, 2880, "SiLU", True)])
+def test_mlp_bf16_weights(dev, T, H, I, act, bias):
+    """Dense mlp with quantization NONE (bf16 gate_w / up_w [H, I], down_w [I, H]) against
+    the reference's torch flow (mlp.py:371-418)."""
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.enums import QuantizationType
+    from vllm_neuron_amd.functional import mlp
+
+    from oracle import mlp as om
+
+    print(f"mlp bf16 T={T} H={H} I={I} {act}", flush=True)
+    g = torch.Generator().manual_seed(110 + T)
+    r = lambda *s, std: (torch.randn(*s, generator=g) * std).to(torch.bfloat16)  # noqa: E731
+    gw, uw, dw = r(H, I, std=H ** -0.5), r(H, I, std=H ** -0.5), r(I, H, std=I ** -0.5)
+    gb, ub, db = (r(1, I, std=0.1), r(1, I, std=0.1), r(1, H, std=0.1)) if bias else (None,) * 3
+    x = synthetic.tokens(111, T, H)
+    mv = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    got = mlp(x.to(dev), mv(gw), mv(uw), mv(dw), act_fn=act, gate_b=mv(gb), up_b=mv(ub),
+              down_b=mv(db), quantization_type=QuantizationType.NONE).cpu()
+    want = om.torch_mlp_impl(x, gw, uw, dw, act, gb, ub, db)
+    assert got.dtype == torch.bfloat16 and got.shape == (T, H)
+    check_close(got.float(), want.float(), None, f"mlp bf16 T={T} H={H} I={I}")
+
+
+def test_decode_operators_reject_bf16_weights(dev):
+    """The decode operators take MXFP4 experts only, as the reference's decode kernel does
+    (moe_tkg.py:48)."""
+    from vllm_neuron_amd import functional as NF
+
+    gu, dn, _, _ = _bf16_experts(5, 4, 256, 256)
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=dev)
+    aff = torch.zeros(4, 4, device=dev)
+    idx = torch.zeros(4, 2, dtype=torch.int32, device=dev)
+    with pytest.raises(NotImplementedError, match="MXFP4"):
+        NF.moe_tkg(x, gu.to(dev).reshape(4, 256, 2, 256), dn.to(dev), aff, idx,
+                   is_all_expert=False)

@@ -18,7 +18,7 @@ ACT_SILU, ACT_GELU, ACT_SWISH = 0, 1, 2
 SCALE_POST, SCALE_NO, SCALE_PRE, SCALE_PRE_DELAYED = 0, 1, 2, 3
 ROUTER_SOFTMAX, ROUTER_SIGMOID = 0, 1
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
-WFMT_MXFP4, WFMT_MXFP8 = 0, 1
+WFMT_MXFP4, WFMT_MXFP8, WFMT_BF16 = 0, 1, 2
 
 _P = C.c_void_p
 _I64 = C.c_int64

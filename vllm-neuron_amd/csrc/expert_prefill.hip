@@ -44,10 +44,10 @@
 
 #include "capi_util.h"
 #include "common.h"
+#include "prefill_common.h"
 
 namespace mxmoe {
 
-constexpr int kPM = 128;      // slots per M-tile
 constexpr int kPWaves = 4;
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kPDma = kPM / kPWaves / 4;      // direct loads (1 KiB = 4 rows) per wave and chunk
@@ -66,69 +66,6 @@ struct PFmt {
 constexpr int kPBw = 4;  // 16-B weight registers per chunk and wave
 constexpr int kPStages = 2;   // activation chunks in LDS (2 or 4)
 constexpr int kPLead = kPStages - 1;  // chunks the direct loads run ahead
-
-struct PrefillArgs {
-  const uint16_t* a;      // x [T, H] (gate_up) or h [slots, I] (down)
-  const uint8_t* wq;      // packed weights, all experts
-  const uint8_t* ws;      // packed scales
-  const uint16_t* bias;   // gate_up: [E, 2, I]; down: [E, H]; may be null
-  const int32_t* tp2id;   // token_position_to_id [slots]
-  uint16_t* out;          // h [slots, I] or y [slots, H]
-  int T, K, N_rows, I, H, B;
-  int n_mtiles, n_ntiles;
-  int group;              // M-tiles scheduled together (divides n_mtiles)
-  const int2* order;      // (first M-tile of a group, its expert) by rank (null: rank order,
-                          // expert 0)
-  int E;                  // experts: a tile whose expert lies outside [0, E) computes nothing
-  int a_by_slot;          // gate_up reads row `slot` of a (pre-scaled rows), not the token's
-  int32_t* inv;           // gate_up, N-tile 0: inv[token * E + expert] = slot (null: none)
-  ExpertParams p;
-};
-
-// Workgroups per GEMM launch: every XCD runs the same number of group ranks.
-inline unsigned prefill_grid(int n_mtiles, int n_ntiles, int group) {
-  const int n_groups = n_mtiles / group;
-  return (unsigned)(8 * group * n_ntiles * ((n_groups + 7) / 8));
-}
-
-// Round to bf16 (nearest even) and back: the gfx950 conversion instruction, which
-// gives round_bf16's result on every non-NaN input (NaN stays NaN).
-__device__ __forceinline__ float rb(float v) { return (float)(__bf16)v; }
-
-// Two floats -> a packed bf16 pair (a low), by the same conversion: one instruction for
-// both.  A NaN stays a NaN; these are intermediates that later kernels read as numbers.
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
-
-__device__ __forceinline__ float clamp_ref(float v, float lo, float hi) {
-  v = (v > hi) ? hi : v;
-  v = (v < lo) ? lo : v;
-  return v;
-}
-
-// Activation on a bf16 value with the reference's bf16 intermediate roundings.  The
-// sigmoid uses the hardware exponential and reciprocal (about 1 ulp each in fp32); its
-// result is rounded to bf16 right after, so it differs from the correctly rounded
-// sigmoid only where that lies within a few fp32 ulps of a bf16 rounding boundary.
-__device__ __forceinline__ float sigmoid_fast(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-}
-
-template <int ACT>
-__device__ __forceinline__ float act_bf16(float g) {
-  if constexpr (ACT == kSwish) {
-    const float t1 = rb(g * 1.702f);
-    const float t2 = rb(sigmoid_fast(t1));
-    return rb(g * t2);
-  } else if constexpr (ACT == kSiLU) {
-    return rb(g * sigmoid_fast(g));
-  } else {
-    return rb(0.5f * g * (1.0f + erff(g * 0.70710678118654752f)));
-  }
-}
 
 // Per-workgroup and per-wave constants of a tile.
 struct PrefillTile {
@@ -735,41 +672,10 @@ __global__ void __launch_bounds__(kPThreads)
     else return sa3;
   };
 
-  // Workgroup -> (XCD, its i-th workgroup) -> (group rank, M-tile in the group, N-tile).
-  // Consecutive workgroups of an XCD go to its shader engines in turn, so each M-tile of
-  // a group takes its N-tiles in a row (alternating M-tiles would send the full tiles to
-  // half of the engines).
-  const int G = args.group, per_group = G * args.n_ntiles;
-  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
-  const int rank = (local / per_group) * 8 + xcd;
-  const int sub = (local % per_group) / args.n_ntiles, nt = local % args.n_ntiles;
-  if (rank >= args.n_mtiles / G) return;
-  int mt = rank * G + sub, e = 0;
-  if (args.order) {
-    const int2 me = args.order[rank];
-    mt = me.x + sub;
-    e = me.y;
-    if (e < 0 || e >= args.E) return;  // a caller's out-of-range expert id: no tile
-  }
-  const int m0 = mt * kPM;
+  PrefillTileId id;
+  if (!prefill_tile_begin<GATE_UP>(args, stok, s_rowoff, s_lastw, id)) return;
+  const int m0 = id.m0, e = id.e, nt = id.nt;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-
-  if (tid < kPM) {  // waves 0 and 1, whole
-    // Without a mapping (plain linear) slot m0 + tid is row m0 + tid of A, real below T.
-    int tk = args.tp2id ? args.tp2id[m0 + tid] : (m0 + tid < args.T ? m0 + tid : -1);
-    if (tk < 0 || tk >= args.T) tk = -1;
-    stok[tid] = tk;
-    // Byte offset of the row's activations.  Padding slots read a real row (token 0 / the
-    // tile's first slot): an MFMA output column depends on its own slot only, and padding
-    // columns are never stored.
-    const uint32_t arow = (GATE_UP && !args.a_by_slot) ? (uint32_t)(tk >= 0 ? tk : 0)
-                                                       : (uint32_t)(tk >= 0 ? m0 + tid : m0);
-    s_rowoff[tid] = arow * (uint32_t)args.K * 2u;
-    // The combine's slot of each (token, expert) pair, written once per M-tile.
-    if (GATE_UP && args.inv && nt == 0 && tk >= 0) args.inv[(size_t)tk * args.E + e] = m0 + tid;
-    const unsigned long long real = __ballot(tk >= 0);
-    if (lane == 0) s_lastw[wave] = real ? 64 * wave + 63 - __builtin_clzll(real) : -1;
-  }
   __syncthreads();
   const int last = max(s_lastw[0], s_lastw[1]);
   if (last < 0) return;
@@ -1148,8 +1054,9 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                              void* workspace, size_t workspace_bytes, void* const* stage_events,
                              void* stream) {
   clear_error();
-  MXMOE_REQUIRE(x && affinities_masked && gu_q && gu_s && dn_q && dn_s && token_position_to_id &&
-                    block_to_expert && out && workspace,
+  const bool bf16w = weight_fmt == MXMOE_WFMT_BF16;
+  MXMOE_REQUIRE(x && affinities_masked && gu_q && dn_q && (bf16w || (gu_s && dn_s)) &&
+                    token_position_to_id && block_to_expert && out && workspace,
                 "moe_cte: null pointer");
   MXMOE_REQUIRE(T >= 1 && E >= 1 && E <= kCteMaxE && n_blocks >= 1,
                 "moe_cte: bad T/E/n_blocks (E at most %d)", kCteMaxE);
@@ -1158,8 +1065,11 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
                 "moe_cte: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
   MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_cte: unknown activation %d", act);
-  MXMOE_REQUIRE(weight_fmt == MXMOE_WFMT_MXFP4 || weight_fmt == MXMOE_WFMT_MXFP8,
+  MXMOE_REQUIRE(weight_fmt == MXMOE_WFMT_MXFP4 || weight_fmt == MXMOE_WFMT_MXFP8 || bf16w,
                 "moe_cte: unknown weight format %d", weight_fmt);
+  // bf16 weight rows are read 16 bytes at a time
+  MXMOE_REQUIRE(!bf16w || ((uintptr_t)gu_q % 16 == 0 && (uintptr_t)dn_q % 16 == 0),
+                "moe_cte: bf16 weights must be 16-byte aligned");
   MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO ||
                     scale_mode == MXMOE_SCALE_PRE || scale_mode == MXMOE_SCALE_PRE_DELAYED,
                 "moe_cte: unsupported scale mode %d", scale_mode);
@@ -1214,12 +1124,15 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.out = w.h;
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
-  a.n_ntiles = prefill_ntiles(2 * I, weight_fmt);
+  a.n_ntiles = bf16w ? prefill_ntiles_bf16(true, I, H) : prefill_ntiles(2 * I, weight_fmt);
   hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
                      (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
                      (int)block_size, a.n_mtiles, a.group, (int)T, w.order);
   mark(0);
-  launch_prefill_gemm(true, weight_fmt, a, s);
+  if (bf16w)
+    launch_prefill_gemm_bf16(true, a, s);
+  else
+    launch_prefill_gemm(true, weight_fmt, a, s);
   mark(1);
   if (delayed)
     hipLaunchKernelGGL(cte_scale_h_kernel, dim3((unsigned)n_slots), dim3(256), 0, s, w.h,
@@ -1235,8 +1148,11 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.out = w.y;
   a.K = (int)I;
   a.N_rows = (int)H;
-  a.n_ntiles = prefill_ntiles(H, weight_fmt);
-  launch_prefill_gemm(false, weight_fmt, a, s);
+  a.n_ntiles = bf16w ? prefill_ntiles_bf16(false, I, H) : prefill_ntiles(H, weight_fmt);
+  if (bf16w)
+    launch_prefill_gemm_bf16(false, a, s);
+  else
+    launch_prefill_gemm(false, weight_fmt, a, s);
   mark(2);
   if (pre || delayed)
     hipLaunchKernelGGL(cte_combine_dense_bf16_kernel,

@@ -1,7 +1,7 @@
-"""Dense MLP with MX (MXFP4 or MXFP8) weights on the MI355X kernels.
+"""Dense MLP with MX (MXFP4 or MXFP8) or bf16 weights on the MI355X kernels.
 
 Mirrors vllm_neuron/functional/mlp.py:29-193 (signature, argument meaning, exception
-types) for ``quantization_type=MX``.  The reference sends that case to the nkilib mlp
+types) for ``quantization_type`` MX and NONE.  The reference sends that case to the nkilib mlp
 kernel (:114-175) and every case it cannot run to its torch flow ``_torch_mlp_impl``
 (:313-418).  Here a dense MLP is the prefill expert path with one expert that every token
 selects at affinity 1: the blockwise mapping of an all-ones [T, 1] affinity column (one
@@ -17,12 +17,16 @@ the reference's ``x @ w`` operand): gate_w and up_w [I/16, 8H] (MXFP4) or [I/16,
 [ceil(H/64), 2I].  gate and up fuse once per tensor version into an expert's gate_up
 (``weights.fuse_gate_up``).  Biases: gate_b, up_b [1, I] or [I]; down_b [1, H] or [H], bf16.
 
+With ``quantization_type=NONE`` the weights are the reference's bf16 operands (gate_w and
+up_w [H, I], down_w [I, H], ``hidden @ w``): gate and up are stacked once per tensor
+version into one expert's gate_up [1, H, 2, I] for the bf16 expert GEMMs.
+
 Activations as the reference's ``_get_activation_fn`` (:261-286): SiLU and Swish are both
 silu here (Swish is not GPT-OSS's 1.702 form in this operator), GELU the exact erf form.
 The clamp limits, which the reference passes to its kernel only, are applied after the
-biases as in moe_cte.  Raised as NotImplementedError: quantization types other than MX
-(dense bf16 or fp8 weights are outside the MX expert path), normalization, the fused
-residual add, skip_gate, static input scales and GELU_Tanh_Approx.
+biases as in moe_cte.  Raised as NotImplementedError: normalization, the fused
+residual add, skip_gate, static input scales and GELU_Tanh_Approx; the FP8 types
+(STATIC, ROW) and non-bf16 weights.
 """
 
 from __future__ import annotations
@@ -90,6 +94,34 @@ def _experts(gate_w, gate_s, up_w, up_s, down_w, down_s, gate_b, up_b, down_b) -
                    (gate_w, gate_s, up_w, up_s, down_w, down_s, gate_b, up_b, down_b), make)
 
 
+def _experts_bf16(gate_w, up_w, down_w, gate_b, up_b, down_b) -> Experts:
+    """bf16 gate_w / up_w [H, I] and down_w [I, H] (the reference's ``x @ w`` operands) as
+    one expert of the bf16 GEMMs: gate_up [1, H, 2, I] (a copy, kept per weight version),
+    down [1, I, H] (a view)."""
+    for t, n in ((gate_w, "gate_w"), (up_w, "up_w"), (down_w, "down_w")):
+        if t.dtype != torch.bfloat16 or t.dim() != 2:
+            raise NotImplementedError(f"{n}: quantization NONE takes bf16 [in, out] weights, got "
+                                      f"{t.dtype} {tuple(t.shape)}")
+    H, I = gate_w.shape
+    if tuple(up_w.shape) != (H, I) or tuple(down_w.shape) != (I, H):
+        raise ValueError(f"gate_w / up_w must be [H, I] and down_w [I, H], got "
+                         f"{tuple(gate_w.shape)}, {tuple(up_w.shape)}, {tuple(down_w.shape)}")
+
+    def make():
+        gu = torch.stack([gate_w, up_w], 1).unsqueeze(0).contiguous()
+        dn = down_w.contiguous().unsqueeze(0)
+        gb, ub, db = _bias(gate_b, I, "gate_b"), _bias(up_b, I, "up_b"), _bias(down_b, H, "down_b")
+        gu_bias = dn_bias = None
+        if gb is not None or ub is not None or db is not None:
+            z = lambda n: torch.zeros(n, dtype=torch.bfloat16, device=gate_w.device)  # noqa: E731
+            gu_bias = torch.stack([z(I) if gb is None else gb, z(I) if ub is None else ub],
+                                  0).unsqueeze(0).contiguous()
+            dn_bias = (z(H) if db is None else db).unsqueeze(0).contiguous()
+        return Experts(gu, None, dn, None, gu_bias, dn_bias, 1, H, I, _lib.WFMT_BF16)
+
+    return derived("mlp_experts_bf16", (gate_w, up_w, down_w, gate_b, up_b, down_b), make)
+
+
 def _identity_mapping(T: int, dev: torch.device):
     """(affinities [T, 1] = 1, token_position_to_id, block_to_expert, n_blocks) of T tokens
     all routed to expert 0, from the mapping kernel; kept per token count and device."""
@@ -125,9 +157,9 @@ def mlp(hidden: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Tensor, eps: float
     """hidden [T, H] bf16 -> [T, H] in ``output_dtype`` (default: hidden's dtype; bf16 or
     float32, the latter being the bf16 result widened)."""
     q = member_name(quantization_type)
-    if q != "MX":
-        raise NotImplementedError(f"mlp with quantization_type {q} has no MI355X kernel (the "
-                                  "MX expert path takes MXFP4 / MXFP8 weights)")
+    if q not in ("MX", "NONE"):
+        raise NotImplementedError(f"mlp with quantization_type {q} has no MI355X kernel (MX "
+                                  "weights, or bf16 ones with NONE)")
     if member_name(norm_type) != "NO_NORM":
         raise NotImplementedError(f"mlp normalization {member_name(norm_type)} is not supported")
     if fused_add_tensor is not None or store_fused_add_result:
@@ -139,12 +171,20 @@ def mlp(hidden: Tensor, gate_w: Tensor, up_w: Tensor, down_w: Tensor, eps: float
     if gate_up_w_layout is not None:
         raise NotImplementedError("mlp gate_up_w_layout selects a Trainium layout")
     act = _act(act_fn)
-    if gate_w_scale is None or up_w_scale is None or down_w_scale is None:
-        raise AssertionError("gate_w_scale, up_w_scale and down_w_scale must be provided for MX "
-                             "quantized compute")
-    dev = _lib.require_cuda(hidden, gate_w, up_w, down_w, gate_w_scale, up_w_scale, down_w_scale)
-    ex = _experts(gate_w, gate_w_scale, up_w, up_w_scale, down_w, down_w_scale, gate_b, up_b,
-                  down_b)
+    if q == "MX":
+        if gate_w_scale is None or up_w_scale is None or down_w_scale is None:
+            raise AssertionError("gate_w_scale, up_w_scale and down_w_scale must be provided "
+                                 "for MX quantized compute")
+        dev = _lib.require_cuda(hidden, gate_w, up_w, down_w, gate_w_scale, up_w_scale,
+                                down_w_scale)
+        ex = _experts(gate_w, gate_w_scale, up_w, up_w_scale, down_w, down_w_scale, gate_b, up_b,
+                      down_b)
+    else:
+        if gate_w_scale is not None or up_w_scale is not None or down_w_scale is not None:
+            raise NotImplementedError("weight scales belong to quantized weights; NONE takes "
+                                      "bf16 weights without scales")
+        dev = _lib.require_cuda(hidden, gate_w, up_w, down_w)
+        ex = _experts_bf16(gate_w, up_w, down_w, gate_b, up_b, down_b)
     H = ex.H
     if hidden.dim() != 2 or hidden.shape[1] != H:
         raise ValueError(f"hidden must be [T, {H}], got {tuple(hidden.shape)}")

@@ -95,15 +95,44 @@ def down_bias(b: Optional[Tensor], E: int, H: int) -> Optional[Tensor]:
 
 class Experts(NamedTuple):
     gu_q: Tensor
-    gu_s: Tensor
+    gu_s: Optional[Tensor]  # None for bf16 weights
     dn_q: Tensor
-    dn_s: Tensor
+    dn_s: Optional[Tensor]
     gu_bias: Optional[Tensor]
     dn_bias: Optional[Tensor]
     E: int
     H: int
     I: int
-    fmt: int = 0  # MXMOE_WFMT_*: 0 MXFP4, 1 MXFP8
+    fmt: int = 0  # MXMOE_WFMT_*: 0 MXFP4, 1 MXFP8, 2 bf16
+
+
+def is_bf16_weights(gate_up_weight: Tensor) -> bool:
+    """Unquantized expert weights (the reference's shard_on_block operands)."""
+    return gate_up_weight.is_floating_point()
+
+
+def resolve_bf16_experts(gu_w: Tensor, dn_w: Tensor, gu_b: Optional[Tensor],
+                         dn_b: Optional[Tensor]) -> Experts:
+    """bf16 expert weights as moe_cte's shard_on_block takes them (moe_cte.py:117-124):
+    gate_up [E, H, 2, I] (or the same memory as [E, H, 2I]: gate columns, then up), down
+    [E, I, H]; biases [E, 2, I] (or [E, 2I]) and [E, H] (or [E, 1, H]).  Used in place
+    (contiguous), no conversion."""
+    for t, n in ((gu_w, "gate_up_proj_weight"), (dn_w, "down_proj_weight")):
+        if t.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{n}: {t.dtype} expert weights have no MI355X kernel "
+                                      "(bf16 or packed MX only)")
+    if dn_w.dim() != 3:
+        raise ValueError(f"down_proj_weight must be [E, I, H], got {tuple(dn_w.shape)}")
+    E, I, H = dn_w.shape
+    if tuple(gu_w.shape) not in ((E, H, 2, I), (E, H, 2 * I)):
+        raise ValueError(f"gate_up_proj_weight must be [{E}, {H}, 2, {I}] (or [{E}, {H}, "
+                         f"{2 * I}]) for down_proj_weight {tuple(dn_w.shape)}, got "
+                         f"{tuple(gu_w.shape)}")
+    gu, dn = gu_w.contiguous(), dn_w.contiguous()
+    if gu.data_ptr() % 16 or dn.data_ptr() % 16:
+        raise ValueError("bf16 expert weights must be 16-byte aligned")
+    return Experts(gu, None, dn, None, gate_up_bias(gu_b, E, I), down_bias(dn_b, E, H), E, H, I,
+                   _lib.WFMT_BF16)
 
 
 def is_neuron_layout(gate_up_weight: Tensor) -> bool:
@@ -162,9 +191,15 @@ def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
 
 def resolve_experts(gu_w: Tensor, gu_s: Optional[Tensor], dn_w: Tensor, dn_s: Optional[Tensor],
                     gu_b: Optional[Tensor], dn_b: Optional[Tensor]) -> Experts:
-    """The expert arguments of moe_cte / moe_tkg / moe_block_tkg in either layout: this
-    build's packed MXFP4 or MXFP8 (uint8, 3-D; biases [E, 2, I] and [E, H]) or the reference's
-    Trainium kernel layout (converted once per tensor version, see _from_neuron_layout)."""
+    """The expert arguments of moe_cte / moe_tkg / moe_block_tkg in any layout: this
+    build's packed MXFP4 or MXFP8 (uint8, 3-D; biases [E, 2, I] and [E, H]), the reference's
+    Trainium kernel layout (converted once per tensor version, see _from_neuron_layout), or
+    bf16 weights (see resolve_bf16_experts; scales must then be absent)."""
+    if is_bf16_weights(gu_w):
+        if gu_s is not None or dn_s is not None:
+            raise NotImplementedError("scaled (FP8) shard_on_block weights have no MI355X "
+                                      "kernel: bf16 weights take no scales")
+        return resolve_bf16_experts(gu_w, dn_w, gu_b, dn_b)
     if is_neuron_layout(gu_w):
         return _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b)
     E, H, I, fmt = expert_shapes(gu_w, gu_s, dn_w, dn_s)
@@ -176,5 +211,6 @@ def require_mxfp4(ex: Experts, what: str) -> None:
     """The decode operators take MXFP4 experts only, as the reference's decode kernel does
     (vllm_neuron/functional/moe/moe_tkg.py:48: "Currently only supports MXFP4 on Trn3")."""
     if ex.fmt != _lib.WFMT_MXFP4:
-        raise NotImplementedError(f"{what}: MXFP8 expert weights are supported by moe_cte only "
+        kind = "bf16" if ex.fmt == _lib.WFMT_BF16 else "MXFP8"
+        raise NotImplementedError(f"{what}: {kind} expert weights are supported by moe_cte only "
                                   "(the reference decode kernel supports MXFP4 only)")

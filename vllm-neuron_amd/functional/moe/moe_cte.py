@@ -6,7 +6,11 @@ meaning, exception types).  The reference dispatches to nkilib moe_cte
 torch flow ``_torch_moe_impl`` (:448-581).  Here every call runs mxmoe_moe_cte:
 the blockwise grouped gate_up GEMM with fused MXFP4 dequant, bias, clamps and
 activation, the down GEMM with bias, and the affinity-weighted combine, with the
-bf16 intermediate roundings of ``_torch_moe_impl``.
+bf16 intermediate roundings of ``_torch_moe_impl``.  bf16 expert weights (the
+shard_on_block operands of the bf16 model, model_bf16.py:1360-1391: gate_up [E, H, 2, I],
+down [E, I, H], no scales) run the same schedule and epilogues on bf16 GEMMs; the MX
+implementations (shard_on_block_mx, shard_on_i_mx, shard_on_i_mx_hybrid) require both
+scales, as the reference asserts (:596-605).
 
 Weights are the packed MXFP4 layout of vllm_neuron_amd.weights: gate_up_proj_weight
 uint8 [E, 2I/16, 8H] with gate_up_proj_scale [E, ceil(2I/64), 2H]; down_proj_weight
@@ -41,7 +45,9 @@ from torch import Tensor
 from ... import _lib
 from ...enums import MoECTEImplementation, QuantizationType, member_name
 from ._cache import derived
-from ._common import act_code, resolve_experts, scale_code
+from ._common import act_code, is_bf16_weights, resolve_experts, scale_code
+
+_MX_IMPLEMENTATIONS = ("shard_on_block_mx", "shard_on_i_mx", "shard_on_i_mx_hybrid")
 
 
 def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_proj_weight: Tensor,
@@ -78,9 +84,16 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
     mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=False, allow_pre=True)
     if gate_up_activations_T is not None or down_activations is not None:
         raise NotImplementedError("activation checkpoint buffers are not supported")
-    if gate_up_proj_scale is None or down_proj_scale is None:
-        raise AssertionError(
-            "gate_up_proj_scale and down_proj_scale must be provided for MX quantized compute")
+    bf16w = is_bf16_weights(gate_up_proj_weight)
+    if member_name(implementation) in _MX_IMPLEMENTATIONS or not bf16w:
+        # moe_cte.py:596-605: the MX implementations need both scales
+        if gate_up_proj_scale is None or down_proj_scale is None:
+            raise AssertionError(
+                "gate_up_proj_scale and down_proj_scale must be provided for MX quantized "
+                "compute")
+        if bf16w:
+            raise ValueError(f"{member_name(implementation)} takes packed MX weights, got "
+                             f"{gate_up_proj_weight.dtype}")
     dev = _lib.require_cuda(hidden_states, expert_affinities_masked, gate_up_proj_weight,
                             down_proj_weight, token_position_to_id, block_to_expert)
     if (gate_and_up_proj_bias is None) != (down_proj_bias is None):
@@ -129,9 +142,10 @@ def _cte_call(x, aff, ex, const, tp2id, b2e, n_blocks, block_size, T, act, clamp
     ws = _lib.workspace(L.mxmoe_moe_cte_workspace_bytes(T, H, I, E, block_size, n_blocks, mode),
                         dev)
     clamps = _lib.clamps_array(*clamp_vals)
+    gu_s = None if ex.gu_s is None else ex.gu_s.contiguous()
+    dn_s = None if ex.dn_s is None else ex.dn_s.contiguous()
     rc = L.mxmoe_moe_cte(x.data_ptr(), aff.data_ptr(), ex.gu_q.contiguous().data_ptr(),
-                         ex.gu_s.contiguous().data_ptr(), ex.dn_q.contiguous().data_ptr(),
-                         ex.dn_s.contiguous().data_ptr(), ex.fmt, _lib.ptr(ex.gu_bias),
+                         _lib.ptr(gu_s), ex.dn_q.contiguous().data_ptr(), _lib.ptr(dn_s), ex.fmt, _lib.ptr(ex.gu_bias),
                          _lib.ptr(ex.dn_bias), _lib.ptr(const), tp2id.data_ptr(), b2e.data_ptr(),
                          n_blocks, block_size, T, H, I, E, act, clamps, mode,
                          int(out.dtype == torch.float32), out.data_ptr(), ws.data_ptr(),
