@@ -240,6 +240,28 @@ int mxmoe_moe_tkg(const uint16_t* x, const int32_t* topk_idx, const float* topk_
                   size_t workspace_bytes, void* const* stage_events, void* stream);
 
 /*
+ * mxmoe_moe_tkg for bf16 expert weights: the decode flow of the reference's torch path
+ * (moe_block_tkg.py:223-297; the bf16 GPT-OSS model's decode call, model_bf16.py:
+ * 1199-1252, passes bf16 weights [E_L, H, 2, I] and [E_L, I, H]) with fp32 intermediates
+ * (h carried as an exact-to-16-bits bf16 pair into the down GEMM) and the ascending-expert
+ * fp32 combine, bf16 output.  The selected experts are mapped blockwise (block 128) and
+ * run the MFMA GEMMs of the bf16 moe_cte path.
+ * Replaces: the nkilib moe_block_tkg / moe_tkg kernels for bf16 weights
+ * (moe_block_tkg.py:474-512, moe_tkg.py:157-190).
+ * x bf16 [T, H]; topk_idx int32 [T, k]; topk_val fp32 [T, k]; expert ids outside [0, E)
+ * are skipped; gu_w bf16 [E, H, 2, I], dn_w bf16 [E, I, H] (16-byte aligned); gu_bias
+ * bf16 [E, 2, I] or NULL, dn_bias bf16 [E, H] or NULL; scale_mode MXMOE_SCALE_POST or
+ * MXMOE_SCALE_NO.
+ */
+size_t mxmoe_moe_tkg_bf16_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                          int top_k);
+int mxmoe_moe_tkg_bf16(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
+                       const uint16_t* gu_w, const uint16_t* dn_w, const uint16_t* gu_bias,
+                       const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
+                       int top_k, int act, const float* clamps, int scale_mode, uint16_t* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Whole decode expert layer in one call: router on x, then the mxmoe_moe_tkg pipeline on
  * the selected experts.  The counterpart of the router + expert stages of nkilib
  * moe_block_tkg (vllm_neuron/functional/moe/moe_block_tkg.py:474-512) for an

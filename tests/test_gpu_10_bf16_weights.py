@@ -1,7 +1,7 @@
-"""bf16 expert weights (the reference's shard_on_block operands, the bf16 GPT-OSS model's
-prefill call model_bf16.py:1360-1391) through moe_cte, and the dense mlp with
-quantization NONE, against the oracle's torch flows on the same bf16 weights
-(moe_cte.py:448-581; mlp.py:371-418).  Bounds: normalized max 2e-2, mean 5e-3
+"""bf16 expert weights (the reference's shard_on_block operands; the bf16 GPT-OSS model's
+prefill call model_bf16.py:1360-1391 and decode call :1199-1252) through moe_cte and
+moe_block_tkg, and the dense mlp with quantization NONE, against the oracle's torch flows
+on the same bf16 weights (moe_cte.py:448-581; moe_block_tkg.py:56-302; mlp.py:371-418).  Bounds: normalized max 2e-2, mean 5e-3
 (tests/moe_helpers.check_close)."""
 
 import pytest
@@ -191,9 +191,9 @@ def test_mlp_bf16_weights(dev, T, H, I, act, bias):
     check_close(got.float(), want.float(), None, f"mlp bf16 T={T} H={H} I={I}")
 
 
-def test_decode_operators_reject_bf16_weights(dev):
-    """The decode operators take MXFP4 experts only, as the reference's decode kernel does
-    (moe_tkg.py:48)."""
+def test_moe_tkg_rejects_bf16_weights(dev):
+    """moe_tkg takes MXFP4 experts only and raises for any other weights, as the reference
+    does (moe_tkg.py:48, :191-194); moe_block_tkg takes bf16 experts (below)."""
     from vllm_neuron_amd import functional as NF
 
     gu, dn, _, _ = _bf16_experts(5, 4, 256, 256)
@@ -203,3 +203,84 @@ def test_decode_operators_reject_bf16_weights(dev):
     with pytest.raises(NotImplementedError, match="MXFP4"):
         NF.moe_tkg(x, gu.to(dev).reshape(4, 256, 2, 256), dn.to(dev), aff, idx,
                    is_all_expert=False)
+
+
+@pytest.mark.parametrize("T,E,k,H,I,act,pre_norm,scale", [
+    (1, 16, 4, 512, 384, "SOFTMAX", False, "POST_SCALE"),
+    (7, 8, 2, 416, 288, "SIGMOID", True, "NO_SCALE"),       # K and N tails in both GEMMs
+    (64, 16, 4, 512, 384, "SOFTMAX", False, "POST_SCALE"),
+])
+def test_moe_block_tkg_bf16_weights(dev, T, E, k, H, I, act, pre_norm, scale):
+    """moe_block_tkg with bf16 experts against the oracle's dense torch flow
+    (moe_block_tkg.py:56-302: fp32 expert math over every expert, the output cast to
+    bf16)."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import moe_block_tkg as obt
+
+    print(f"moe_block_tkg bf16 T={T} E={E} k={k} H={H} I={I} {act} {scale}", flush=True)
+    gu, dn, gb, db = _bf16_experts(120 + T, E, H, I)
+    x = synthetic.tokens(121 + T, T, H)
+    gamma = 1.0 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(122))
+    rw = synthetic.normal_bf16(123, (H, E), 0.05)
+    clamps = dict(gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                  up_clamp_lower_limit=-6.0)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    out, logits = NF.moe_block_tkg(
+        x.unsqueeze(0).to(dev), mv(gamma).unsqueeze(0), mv(rw), mv(gu).reshape(E, H, 2, I),
+        mv(dn), top_k=k, expert_gate_up_bias=mv(gb).reshape(E, 2, I), expert_down_bias=mv(db),
+        router_act_fn=act, router_pre_norm=pre_norm, expert_affinities_scaling_mode=scale,
+        hidden_act_fn="Swish", **clamps)
+    want, logits_r = obt.torch_moe_block_tkg_impl(
+        x, gamma, rw, gu.reshape(E, H, 2, I), dn, expert_gate_up_bias=gb.reshape(E, 2, I),
+        expert_down_bias=db, top_k=k, router_act_fn=act, router_pre_norm=pre_norm,
+        expert_affinities_scaling_mode=scale, hidden_act_fn="Swish", **clamps)
+    assert out.dtype == torch.bfloat16 and out.shape == (T, H)
+    assert torch.allclose(logits.cpu(), logits_r, rtol=1e-5, atol=1e-5)
+    check_close(out.cpu().float(), want.float(), None, f"moe_block_tkg bf16 T={T} {scale}")
+
+
+def test_bf16_model_decode_call(dev):
+    """The bf16 GPT-OSS model's decode MoE (model_bf16.py:1199-1252) with its argument list:
+    padded H = I = 3072 with hidden_actual = 2880, fp32 gamma [1, H], router_weight.T, the
+    bias views, softmax routing after top-k, clamped Swish; against the oracle's RMSNorm +
+    router and its fp32 expert flow on the selected experts."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.enums import ActFnType, ExpertAffinityScaleMode, RouterActFnType
+
+    from oracle import moe_block_tkg as obt
+
+    E, k, H, I, ha, T, limit = 8, 4, 3072, 3072, 2880, 16, 7.0
+    gu, dn, gb, db = _bf16_experts(130, E, H, I)
+    x = synthetic.tokens(131, T, H)
+    x[:, ha:] = 0
+    ln_w = (1.0 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(132))).to(
+        torch.bfloat16)
+    router_weight = synthetic.normal_bf16(133, (E, H), 0.05)
+    router_bias = synthetic.normal_bf16(134, (E,), 0.05)
+    mv = lambda t: t.to(dev)  # noqa: E731
+    out = NF.moe_block_tkg(
+        inp=x.to(dev).unsqueeze(0), gamma=mv(ln_w).unsqueeze(0).to(torch.float32),
+        router_weights=mv(router_weight).T, expert_gate_up_weights=mv(gu).reshape(E, H, 2, I),
+        expert_down_weights=mv(dn), rank_id=None, top_k=k,
+        router_bias=mv(router_bias).unsqueeze(0),
+        expert_gate_up_bias=mv(gb).reshape(E, 2, I), expert_down_bias=mv(db), eps=1e-5,
+        router_act_fn=RouterActFnType.SOFTMAX, router_pre_norm=False,
+        expert_affinities_scaling_mode=ExpertAffinityScaleMode.POST_SCALE,
+        hidden_act_fn=ActFnType.Swish, gate_clamp_upper_limit=limit,
+        gate_clamp_lower_limit=None, up_clamp_upper_limit=limit + 1,
+        up_clamp_lower_limit=-limit + 1, router_mm_dtype="bfloat16", hidden_actual=ha,
+        is_all_expert=False, skip_router_logits=True)
+    xn, _, top, idx = obt.rmsnorm_router(x, ln_w.float(), router_weight.T, router_bias, 1e-5, k,
+                                         "SOFTMAX", False, False, hidden_actual=ha)
+    aff = torch.zeros(T, E).scatter_(1, idx, top)
+    want = obt.expert_mlp_fp32_routed(xn, aff, gu.reshape(E, H, 2, I), dn, gb.reshape(E, 2, I),
+                                      db, hidden_act_fn="Swish", gate_clamp_upper_limit=limit,
+                                      up_clamp_upper_limit=limit + 1,
+                                      up_clamp_lower_limit=-limit + 1, scale_mode="POST_SCALE",
+                                      out_dtype=torch.bfloat16)
+    got = out.cpu()
+    assert got.shape == (T, H)
+    check_close(got.float(), want.float(), None, "bf16 model decode call")

@@ -49,6 +49,9 @@ _SIGNATURES = {
     "mxmoe_moe_tkg_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
                            _I, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_tkg_bf16_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
+    "mxmoe_moe_tkg_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
+                                _I, _P, _P, _SZ, _P]),
     "mxmoe_moe_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_decode": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I64,
                               _I64, _I64, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _SZ, _P, _P]),

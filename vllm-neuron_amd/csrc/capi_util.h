@@ -58,6 +58,17 @@ int router_run(const RouterSpec& r, int64_t T, int64_t H, int64_t E, int top_k, 
 int rmsnorm_run(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t ha,
                 int all_cols, float eps, int out_dt, uint16_t* out, hipStream_t s);
 
+// Blocks of the blockwise mapping of T tokens with top_k experts each over E experts at
+// block size B: the reference's bound (moe_blockwise.py:343-349), at most one block per
+// routed slot.
+inline int64_t blockwise_n_blocks(int64_t T, int64_t E, int top_k, int64_t B) {
+  const int64_t total = T * (top_k < E ? top_k : E);
+  int64_t nb = (total - (E - 1) + B - 1) / B;
+  if (total - (E - 1) <= 0) nb = (total - (E - 1)) / B;  // ceil of a non-positive value
+  nb += E - 1;
+  return nb > total ? total : nb;
+}
+
 // Bump allocator over a caller-provided workspace.
 struct Carver {
   char* base;

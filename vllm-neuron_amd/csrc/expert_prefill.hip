@@ -860,8 +860,9 @@ __device__ __forceinline__ int cte_slot_of(const int32_t* __restrict__ inv,
 constexpr int kCombineThreads = 256;
 constexpr int kCombineTok = kCombineThreads / 64;
 constexpr int kCteMaxE = 1024;
+template <typename YT>  // y element: bf16 bits (prefill flow) or fp32 (decode flow)
 __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
-    const uint16_t* __restrict__ y, const int32_t* __restrict__ inv,
+    const YT* __restrict__ y, const int32_t* __restrict__ inv,
     const int32_t* __restrict__ tp2id, const int32_t* __restrict__ b2e, int64_t n_slots, int B,
     const float* __restrict__ aff, int T, int H, int E, int scale_mode, int out_f32,
     void* __restrict__ out) {
@@ -893,9 +894,23 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
 #pragma unroll 4
     for (int k = 0; k < cnt; ++k) {
       const float a = s_w[wave][k];
-      const u16x8 v = *reinterpret_cast<const u16x8*>(y + (size_t)s_slot[wave][k] * H + n);
+      const YT* row = y + (size_t)s_slot[wave][k] * H + n;
+      float v[8];
+      if constexpr (sizeof(YT) == 2) {
+        const u16x8 b = *reinterpret_cast<const u16x8*>(row);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(v[i]), a));
+        for (int i = 0; i < 8; ++i) v[i] = bf16_bits_to_f32(b[i]);
+      } else {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(row);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(row + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = lo[i];
+          v[4 + i] = hi[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], a));
     }
     if (out_f32) {
       float* o = static_cast<float*>(out) + (size_t)t * H + n;
@@ -1033,9 +1048,149 @@ static void launch_prefill_gemm(bool gate_up, int fmt, const PrefillArgs& a, hip
   }
 }
 
+// Decode with bf16 expert weights: the routed top-k as dense affinities [T, E] (zero
+// where not selected; expert ids outside [0, E) skipped), one workgroup per token.
+__global__ void __launch_bounds__(256) tkg_bf16_scatter_kernel(const int32_t* __restrict__ idx,
+                                                               const float* __restrict__ val,
+                                                               int E, int K, float* __restrict__ aff) {
+  const int t = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 256) aff[(size_t)t * E + e] = 0.0f;
+  __syncthreads();
+  if (threadIdx.x < K) {
+    const int e = idx[(size_t)t * K + threadIdx.x];
+    if (e >= 0 && e < E) aff[(size_t)t * E + e] = val[(size_t)t * K + threadIdx.x];
+  }
+}
+
+constexpr int kTkgBf16Block = 128;  // one M-tile per block: decode batches are small
+struct TkgBf16Ws {
+  float *aff, *aff_m;
+  int32_t *tp2id, *b2e, *cond, *inv;
+  void* bw;
+  size_t bw_bytes;
+  int2* order;
+  uint16_t *h_hi, *h_lo;
+  float* y;
+  int64_t n_blocks;
+};
+
+static size_t tkg_bf16_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
+                             int K, TkgBf16Ws* w) {
+  Carver cv(base, cap);
+  TkgBf16Ws c;
+  c.n_blocks = blockwise_n_blocks(T, E, K, kTkgBf16Block);
+  const int64_t n_slots = c.n_blocks * kTkgBf16Block;
+  c.aff = cv.take<float>(T * E);
+  c.aff_m = cv.take<float>(T * E);
+  c.tp2id = cv.take<int32_t>(n_slots);
+  c.b2e = cv.take<int32_t>(c.n_blocks);
+  c.cond = cv.take<int32_t>(c.n_blocks);
+  c.inv = cv.take<int32_t>(T * E);
+  c.bw_bytes = mxmoe_blockwise_workspace_bytes(T, E);
+  c.bw = cv.take<char>(c.bw_bytes);
+  c.order = cv.take<int2>(n_slots / kPM);
+  c.h_hi = cv.take<uint16_t>(n_slots * I);
+  c.h_lo = cv.take<uint16_t>(n_slots * I);
+  c.y = cv.take<float>(n_slots * H);
+  if (w) *w = c;
+  return cv.off + 256;
+}
+
 }  // namespace mxmoe
 
 using namespace mxmoe;
+
+extern "C" size_t mxmoe_moe_tkg_bf16_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
+                                                     int top_k) {
+  if (T < 1 || E < 1 || top_k < 1) return 256;
+  return tkg_bf16_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
+}
+
+extern "C" int mxmoe_moe_tkg_bf16(const uint16_t* x, const int32_t* topk_idx,
+                                  const float* topk_val, const uint16_t* gu_w,
+                                  const uint16_t* dn_w, const uint16_t* gu_bias,
+                                  const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I,
+                                  int64_t E, int top_k, int act, const float* clamps,
+                                  int scale_mode, uint16_t* out, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  clear_error();
+  MXMOE_REQUIRE(x && topk_idx && topk_val && gu_w && dn_w && out && workspace,
+                "moe_tkg_bf16: null pointer");
+  MXMOE_REQUIRE(T >= 1 && E >= 1 && E <= kCteMaxE && top_k >= 1 && top_k <= 256,
+                "moe_tkg_bf16: bad T/E/top_k (E at most %d, top_k at most 256)", kCteMaxE);
+  MXMOE_REQUIRE(H % 32 == 0 && I % 32 == 0 && H >= 32 && I >= 32,
+                "moe_tkg_bf16: H=%lld and I=%lld must be multiples of 32", (long long)H,
+                (long long)I);
+  MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_tkg_bf16: unknown activation %d", act);
+  MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
+                "moe_tkg_bf16: unsupported scale mode %d", scale_mode);
+  MXMOE_REQUIRE((uintptr_t)gu_w % 16 == 0 && (uintptr_t)dn_w % 16 == 0,
+                "moe_tkg_bf16: bf16 weights must be 16-byte aligned");
+  const int64_t n_slots = blockwise_n_blocks(T, E, top_k, kTkgBf16Block) * kTkgBf16Block;
+  const int64_t kmax = H > I ? H : I;
+  MXMOE_REQUIRE(n_slots / kPM <= kOrderMaxTiles && n_slots * kmax * 2 < ((int64_t)1 << 32) &&
+                    T * H * 2 < ((int64_t)1 << 32),
+                "moe_tkg_bf16: %lld tokens x %d experts exceed one call", (long long)T, top_k);
+  const size_t need = tkg_bf16_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
+  if (workspace_bytes < need)
+    return set_error(MXMOE_E_WORKSPACE, "moe_tkg_bf16: workspace %zu < %zu", workspace_bytes,
+                     need);
+  TkgBf16Ws w;
+  tkg_bf16_carve(workspace, workspace_bytes, T, H, I, E, top_k, &w);
+  hipStream_t s = as_stream(stream);
+
+  hipLaunchKernelGGL(tkg_bf16_scatter_kernel, dim3((unsigned)T), dim3(256), 0, s, topk_idx,
+                     topk_val, (int)E, top_k, w.aff);
+  int rc = mxmoe_blockwise_mapping(w.aff, nullptr, T, E, top_k, kTkgBf16Block, w.n_blocks,
+                                   w.aff_m, w.tp2id, w.b2e, w.cond, nullptr, w.bw, w.bw_bytes,
+                                   stream);
+  if (rc != MXMOE_OK) return rc;
+
+  PrefillArgs a = {};
+  a.tp2id = w.tp2id;
+  a.T = (int)T;
+  a.I = (int)I;
+  a.H = (int)H;
+  a.B = kTkgBf16Block;
+  a.n_mtiles = (int)(n_slots / kPM);
+  a.group = prefill_group_tiles(kTkgBf16Block);
+  a.order = w.order;
+  a.E = (int)E;
+  a.a_by_slot = 0;
+  a.inv = w.inv;
+  a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
+  a.p.gate_hi = clamps ? clamps[1] : INFINITY;
+  a.p.up_lo = clamps ? clamps[2] : -INFINITY;
+  a.p.up_hi = clamps ? clamps[3] : INFINITY;
+  a.p.act = act;
+  hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
+                     (size_t)a.n_mtiles * 5, s, w.tp2id, w.b2e, kTkgBf16Block, a.n_mtiles,
+                     a.group, (int)T, w.order);
+  // gate_up: A = x (K = H), rows = 2I; h as (hi, lo)
+  a.a = x;
+  a.wq = reinterpret_cast<const uint8_t*>(gu_w);
+  a.bias = gu_bias;
+  a.out = w.h_hi;
+  a.K = (int)H;
+  a.N_rows = (int)(2 * I);
+  a.n_ntiles = prefill_ntiles_bf16(true, I, H);
+  launch_decode_gemm_bf16(true, a, nullptr, w.h_lo, nullptr, s);
+  // down: A = h (K = I) in two passes, rows = H; y fp32
+  a.a = w.h_hi;
+  a.inv = nullptr;
+  a.wq = reinterpret_cast<const uint8_t*>(dn_w);
+  a.bias = dn_bias;
+  a.out = nullptr;
+  a.K = (int)I;
+  a.N_rows = (int)H;
+  a.n_ntiles = prefill_ntiles_bf16(false, I, H);
+  launch_decode_gemm_bf16(false, a, w.h_lo, nullptr, w.y, s);
+  hipLaunchKernelGGL(cte_combine_kernel<float>,
+                     dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
+                     dim3(kCombineThreads), 0, s, w.y, w.inv, w.tp2id, w.b2e, n_slots,
+                     kTkgBf16Block, w.aff, (int)T, (int)H, (int)E, scale_mode, 0, out);
+  return check_launch("moe_tkg_bf16");
+}
 
 extern "C" size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                                 int64_t block_size, int64_t n_blocks,
@@ -1160,7 +1315,8 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                        w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
                        expert_const, (int)H, (int)E, out_f32, out);
   else
-    hipLaunchKernelGGL(cte_combine_kernel, dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
+    hipLaunchKernelGGL(cte_combine_kernel<uint16_t>,
+                       dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
                        dim3(kCombineThreads), 0, s, w.y, w.inv, token_position_to_id,
                        block_to_expert, n_slots, (int)block_size, affinities_masked, (int)T,
                        (int)H, (int)E, scale_mode, out_f32, out);

@@ -21,6 +21,11 @@
 // workgroup: two workgroups per CU.
 // gate_up N-tile: 64 intermediate columns as 4 pairs of 16-column tiles (gate, up) so
 // that a lane holds gate and up of the same columns; down N-tile: 128 columns of H.
+// Two flows share the GEMMs (template F32):
+//   prefill (moe_cte, moe_cte.py:448-581): the bf16 result of every op, h bf16, y bf16;
+//   decode (moe_block_tkg.py:223-297): fp32 throughout; gate_up writes h as an exact-to-
+//   16-bits pair hi + lo of bf16 arrays, the down GEMM runs K twice (hi rows, then lo
+//   rows against the same weight rows: bf16 products are exact in fp32) and writes y fp32.
 
 #include <math.h>
 
@@ -37,6 +42,14 @@ constexpr int kBThreads = 256;
 constexpr int kBGateUpCols = kBN / 2;  // intermediate columns of a gate_up N-tile
 static_assert(kBThreads == 16 * 16, "one 8 x 8 weight block per thread and chunk");
 static_assert(kPM * (kBRow / 16) == 8 * kBThreads, "8 activation blocks per thread and chunk");
+
+// The decode flow's extra operands (null in the prefill flow).
+struct Bf16Args {
+  PrefillArgs p;
+  const uint16_t* a_lo;  // down: lo part of h [slots, I]
+  uint16_t* out_lo;      // gate_up: lo part of h [slots, I]
+  float* y32;            // down: y [slots, H] fp32
+};
 
 // LDS byte offset of 16-byte block `blk` (0..15) of row `row`.
 __device__ __forceinline__ uint32_t bsw(int row, int blk) {
@@ -192,9 +205,87 @@ __device__ __forceinline__ void bf16_down_store(const PrefillArgs& args, const f
   }
 }
 
-template <bool GATE_UP>
+__device__ __forceinline__ float clamp_f32(float v, float lo, float hi) {
+  v = (v > hi) ? hi : v;  // torch.clamp: NaN stays NaN
+  v = (v < lo) ? lo : v;
+  return v;
+}
+
+// The decode flow's activation in fp32 (moe_block_tkg.py:250-263).
+__device__ __forceinline__ float act_fp32(float g, int act) {
+  if (act == kSwish) return g * (1.0f / (1.0f + expf(-(g * 1.702f))));
+  if (act == kSiLU) return g / (1.0f + expf(-g));
+  return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+}
+
+// Decode-flow gate_up epilogue: fp32 bias, clamps and activation, h = up * act(gate) as
+// the bf16 pair (hi, lo).
+__device__ __forceinline__ void bf16_gate_up_store_f32(const Bf16Args& b, const f32x4 (&acc)[4][4],
+                                                       const int32_t* stok, int m0, int e, int c0,
+                                                       int sh) {
+  const PrefillArgs& args = b.p;
+  const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
+  const int I = args.I;
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+    const int col0 = c0 + 16 * pp + 4 * lq;
+    if (col0 >= I) continue;
+    float gb[4] = {0.f, 0.f, 0.f, 0.f}, ub[4] = {0.f, 0.f, 0.f, 0.f};
+    if (args.bias) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        gb[i] = bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + col0 + i]);
+        ub[i] = bf16_bits_to_f32(args.bias[(size_t)e * 2 * I + I + col0 + i]);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = 64 * sh + 16 * s + li;
+      if (stok[row] < 0) continue;
+      uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g = clamp_f32(acc[2 * pp][s][i] + gb[i], args.p.gate_lo, args.p.gate_hi);
+        const float u = clamp_f32(acc[2 * pp + 1][s][i] + ub[i], args.p.up_lo, args.p.up_hi);
+        split_bf16(u * act_fp32(g, args.p.act), hi[i], lo[i]);
+      }
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      const size_t o = (size_t)(m0 + row) * I + col0;
+      *reinterpret_cast<u16x4*>(args.out + o) = u16x4{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<u16x4*>(b.out_lo + o) = u16x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+  }
+}
+
+// Decode-flow down epilogue: y = acc + bias in fp32.
+__device__ __forceinline__ void bf16_down_store_f32(const Bf16Args& b, const f32x4 (&acc)[4][4],
+                                                    const int32_t* stok, int m0, int e, int n0,
+                                                    int sh) {
+  const PrefillArgs& args = b.p;
+  const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
+  const int H = args.H;
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int n = n0 + 16 * f + 4 * lq;
+    if (n >= H) continue;
+    f32x4 bb = {0.f, 0.f, 0.f, 0.f};
+    if (args.bias) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bb[i] = bf16_bits_to_f32(args.bias[(size_t)e * H + n + i]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = 64 * sh + 16 * s + li;
+      if (stok[row] < 0) continue;
+      *reinterpret_cast<f32x4*>(b.y32 + (size_t)(m0 + row) * H + n) = acc[f][s] + bb;
+    }
+  }
+}
+
+template <bool GATE_UP, bool F32>
 __global__ void __launch_bounds__(kBThreads)
-    __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_bf16_kernel(PrefillArgs args) {
+    __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_bf16_kernel(Bf16Args bargs) {
+  const PrefillArgs& args = bargs.p;
   __shared__ __attribute__((aligned(1024))) uint8_t s_a[kPM * kBRow], s_w[kBN * kBRow];
   __shared__ int32_t stok[kPM];
   __shared__ uint32_t s_rowoff[kPM];
@@ -238,13 +329,22 @@ __global__ void __launch_bounds__(kBThreads)
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[f][s] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int nc = (K + kBK - 1) / kBK;
+  // The decode flow's down GEMM runs its chunks twice: hi rows of h, then lo rows.
+  constexpr bool TWO = F32 && !GATE_UP;
+  const int ncc = TWO ? 2 * nc : nc;
+  const char* abase_lo = TWO ? reinterpret_cast<const char*>(bargs.a_lo) : abase;
   BChunk r;
   bf16_load<GATE_UP>(r, abase, aoff, wbase, wcol_ok, ldw, K, 0);
   bf16_store_lds(r, s_a, s_w);
   __syncthreads();
-  for (int c = 0; c < nc; ++c) {
-    const bool more = c + 1 < nc;
-    if (more) bf16_load<GATE_UP>(r, abase, aoff, wbase, wcol_ok, ldw, K, (c + 1) * kBK);
+  for (int c = 0; c < ncc; ++c) {
+    const bool more = c + 1 < ncc;
+    if (more) {
+      const int cn = c + 1;
+      const bool lo = TWO && cn >= nc;
+      bf16_load<GATE_UP>(r, lo ? abase_lo : abase, aoff, wbase, wcol_ok, ldw, K,
+                         (lo ? cn - nc : cn) * kBK);
+    }
     if (active) bf16_compute(s_a, s_w, fh, sh, acc);
     __syncthreads();
     if (more) {
@@ -253,6 +353,13 @@ __global__ void __launch_bounds__(kBThreads)
     }
   }
   if (!active) return;
+  if constexpr (F32) {
+    if (GATE_UP)
+      bf16_gate_up_store_f32(bargs, acc, stok, m0, e, nt * kBGateUpCols + 32 * fh, sh);
+    else
+      bf16_down_store_f32(bargs, acc, stok, m0, e, nt * kBN + 64 * fh, sh);
+    return;
+  }
   if (GATE_UP) {
     const int c0 = nt * kBGateUpCols + 32 * fh;
     if (args.p.act == kSwish)
@@ -272,10 +379,21 @@ int prefill_ntiles_bf16(bool gate_up, int64_t I, int64_t H) {
 
 void launch_prefill_gemm_bf16(bool gate_up, const PrefillArgs& a, hipStream_t s) {
   const dim3 g(prefill_grid(a.n_mtiles, a.n_ntiles, a.group));
+  const Bf16Args b = {a, nullptr, nullptr, nullptr};
   if (gate_up)
-    hipLaunchKernelGGL(prefill_gemm_bf16_kernel<true>, g, dim3(kBThreads), 0, s, a);
+    hipLaunchKernelGGL((prefill_gemm_bf16_kernel<true, false>), g, dim3(kBThreads), 0, s, b);
   else
-    hipLaunchKernelGGL(prefill_gemm_bf16_kernel<false>, g, dim3(kBThreads), 0, s, a);
+    hipLaunchKernelGGL((prefill_gemm_bf16_kernel<false, false>), g, dim3(kBThreads), 0, s, b);
+}
+
+void launch_decode_gemm_bf16(bool gate_up, const PrefillArgs& a, const uint16_t* a_lo,
+                             uint16_t* out_lo, float* y32, hipStream_t s) {
+  const dim3 g(prefill_grid(a.n_mtiles, a.n_ntiles, a.group));
+  const Bf16Args b = {a, a_lo, out_lo, y32};
+  if (gate_up)
+    hipLaunchKernelGGL((prefill_gemm_bf16_kernel<true, true>), g, dim3(kBThreads), 0, s, b);
+  else
+    hipLaunchKernelGGL((prefill_gemm_bf16_kernel<false, true>), g, dim3(kBThreads), 0, s, b);
 }
 
 }  // namespace mxmoe

@@ -175,11 +175,7 @@ extern "C" int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* p
   MXMOE_REQUIRE(T >= 1 && E >= 1 && E <= kMaxE, "blockwise_mapping: T=%lld E=%lld out of range",
                 (long long)T, (long long)E);
   MXMOE_REQUIRE(block_size >= 1 && top_k >= 1, "blockwise_mapping: bad block_size/top_k");
-  const int64_t total = T * (top_k < E ? top_k : E);
-  int64_t nb = (total - (E - 1) + block_size - 1) / block_size;
-  if (total - (E - 1) <= 0) nb = (total - (E - 1)) / block_size;  // ceil of a non-positive value
-  nb += E - 1;
-  if (nb > total) nb = total;
+  const int64_t nb = blockwise_n_blocks(T, E, top_k, block_size);
   MXMOE_REQUIRE(n_blocks == nb, "blockwise_mapping: n_blocks=%lld, expected %lld",
                 (long long)n_blocks, (long long)nb);
   if (workspace_bytes < bw_ws(T, E))

@@ -127,6 +127,10 @@ __device__ __forceinline__ float act_bf16(float g) {
 // gate_up / down GEMM of bf16 expert weights ([E, H, 2, I] and [E, I, H], K-major rows as
 // the reference's shard_on_block passes them) over the same schedule and epilogues.
 void launch_prefill_gemm_bf16(bool gate_up, const PrefillArgs& a, hipStream_t s);
+// The same GEMMs with the decode flow's fp32 arithmetic: gate_up writes h as bf16 (hi in
+// a.out, lo in out_lo); down reads h from a.a (hi) and a_lo (lo) and writes y32 fp32.
+void launch_decode_gemm_bf16(bool gate_up, const PrefillArgs& a, const uint16_t* a_lo,
+                             uint16_t* out_lo, float* y32, hipStream_t s);
 int prefill_ntiles_bf16(bool gate_up, int64_t I, int64_t H);
 
 }  // namespace mxmoe

@@ -8,7 +8,9 @@ columns, result cast to the input dtype as :134-150), the router on the normaliz
 rows (fp32 logits, router_pre_norm / norm_topk_prob as :152-204), then the experts (fp32
 expert math over the selected experts, ascending-id fp32 sum, cast to the input dtype).
 With a slice of the experts (rank_id), the same steps as mxmoe_rmsnorm,
-mxmoe_router_topk and mxmoe_moe_tkg on the local expert ids.
+mxmoe_router_topk and mxmoe_moe_tkg on the local expert ids.  bf16 expert weights (the
+bf16 model's call, model_bf16.py:1199-1252: gate_up [E_L, H, 2, I], down [E_L, I, H])
+take those steps with mxmoe_moe_tkg_bf16 for the experts.
 
 Shared experts, fused residual add and activation quantization have no MI355X
 kernel and raise NotImplementedError, like the reference's torch flow does for
@@ -26,7 +28,7 @@ from ... import _lib
 from ...enums import ActFnType, ExpertAffinityScaleMode, RouterActFnType, member_name
 from ._cache import transposed_rows
 from ._common import act_code, require_mxfp4, resolve_experts, scale_code
-from .moe_tkg import moe_tkg_raw
+from .moe_tkg import moe_tkg_bf16_raw, moe_tkg_raw
 from .router import rms_norm, router_topk_raw
 
 
@@ -103,8 +105,9 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
                   is_all_expert: bool = False,
                   residual: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
     """inp bf16 [B, S, H] or [T, H]; gamma [1, H] or [H]; router_weights [H, E] (bf16 or
-    fp16); router_bias [1, E] or [E]; expert weights packed (uint8) or in the reference's
-    Trainium MX layout (uint16 [E_L, 128, 2, H/512, I], converted once per tensor version).
+    fp16); router_bias [1, E] or [E]; expert weights packed (uint8), in the reference's
+    Trainium MX layout (uint16 [E_L, 128, 2, H/512, I], converted once per tensor version)
+    or bf16 ([E_L, H, 2, I] and [E_L, I, H]).
     Returns output [T, H] (+ router_logits [T, E] fp32).
 
     router_mm_dtype is accepted and leaves the arithmetic as the reference's torch flow
@@ -125,7 +128,9 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
     ex = resolve_experts(expert_gate_up_weights, expert_gate_up_weights_scale,
                          expert_down_weights, expert_down_weights_scale, expert_gate_up_bias,
                          expert_down_bias)
-    require_mxfp4(ex, "moe_block_tkg")
+    bf16w = ex.fmt == _lib.WFMT_BF16
+    if not bf16w:
+        require_mxfp4(ex, "moe_block_tkg")
     E_L = ex.E
     fn = member_name(router_act_fn)
     if fn == "SOFTMAX":
@@ -141,7 +146,7 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
         raise ValueError(f"router_bias has {bias.numel()} elements, expected {E_g}")
     clamps = _lib.clamps_array(gate_clamp_lower_limit, gate_clamp_upper_limit,
                                up_clamp_lower_limit, up_clamp_upper_limit)
-    if E_L == E_g:
+    if E_L == E_g and not bf16w:
         # Every expert on this rank: RMSNorm, router and experts in one library call.
         out, logits, _ = block_decode_raw(inp, gamma, eps, hidden_actual, router_weights, bias,
                                           act, bool(router_pre_norm), bool(norm_topk_prob),
@@ -154,8 +159,9 @@ def moe_block_tkg(inp: Tensor, gamma: Tensor, router_weights: Tensor,
                                           bool(router_pre_norm), bool(norm_topk_prob), 1e-20)
     if E_L < E_g and rank_id is not None:
         idx = idx - E_L * rank_id.reshape(-1)[0].to(idx.dtype)
-    out = moe_tkg_raw(xn, idx, val, ex, act_code(hidden_act_fn), clamps,
-                      scale_code(expert_affinities_scaling_mode))
+    run = moe_tkg_bf16_raw if bf16w else moe_tkg_raw
+    out = run(xn, idx, val, ex, act_code(hidden_act_fn), clamps,
+              scale_code(expert_affinities_scaling_mode))
     if skip_router_logits:
         return out
     return out, logits

@@ -47,6 +47,27 @@ def moe_tkg_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, ex: Experts, act:
     return out
 
 
+def moe_tkg_bf16_raw(x: Tensor, topk_idx: Tensor, topk_val: Tensor, ex: Experts, act: int,
+                     clamps, scale_mode: int) -> Tensor:
+    """mxmoe_moe_tkg_bf16: the same decode flow on bf16 experts (gate_up [E, H, 2, I], down
+    [E, I, H]), as moe_block_tkg runs it for the bf16 model (model_bf16.py:1199-1252)."""
+    dev = _lib.require_cuda(x, topk_idx, topk_val, ex.gu_q)
+    E, H, I = ex.E, ex.H, ex.I
+    if x.dim() != 2 or x.shape[1] != H:
+        raise ValueError(f"hidden states must be [T, {H}], got {tuple(x.shape)}")
+    T, K = topk_idx.shape
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    ws = _lib.workspace(L.mxmoe_moe_tkg_bf16_workspace_bytes(T, H, I, E, K), dev)
+    rc = L.mxmoe_moe_tkg_bf16(x.contiguous().data_ptr(), topk_idx.contiguous().data_ptr(),
+                              topk_val.contiguous().data_ptr(), ex.gu_q.data_ptr(),
+                              ex.dn_q.data_ptr(), _lib.ptr(ex.gu_bias), _lib.ptr(ex.dn_bias), T,
+                              H, I, E, K, act, clamps, scale_mode, out.data_ptr(), ws.data_ptr(),
+                              ws.numel(), _lib.stream_handle(dev))
+    _lib.check(rc, "mxmoe_moe_tkg_bf16")
+    return out
+
+
 def moe_tkg(hidden_input: Tensor, expert_gate_up_weights: Tensor, expert_down_weights: Tensor,
             expert_affinities: Tensor, expert_index: Tensor, is_all_expert: bool,
             rank_id: Optional[Tensor] = None, expert_gate_up_bias: Optional[Tensor] = None,
