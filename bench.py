@@ -24,6 +24,9 @@ GPU that has been idle reaches its steady clocks only after a few hundred millis
 work, and a short timed region otherwise measures the clock ramp.  The timed region is
 exactly the requested steps.
 
+``--weights bf16`` times the bf16-expert path instead (the reference's shard_on_block
+operands; moe_cte prefill and moe_block_tkg decode) and prints a line of its own.
+
 ``cpu_baseline`` times the CPU oracle (a port of the reference's CPU flow: dense
 all-expert fp32 decode, dense all-expert bf16 prefill) on the host cores over a
 bounded sample of experts / tokens and scales linearly to the full workload.
@@ -72,6 +75,9 @@ def parse():
                     help="seconds of untimed steps after the warmup and again right before "
                          "each timed region, so that the GPU runs at its steady clocks "
                          "(0 disables)")
+    ap.add_argument("--weights", default="mxfp4", choices=["mxfp4", "bf16"],
+                    help="bf16: time the bf16-expert path (moe_cte shard_on_block prefill, "
+                         "moe_block_tkg decode) instead; prints its own line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three device copies of exactly 1 GiB (the reference "
                          "kernel that scales the rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -206,6 +212,101 @@ def cpu_baseline(wl, decode_T, prefill_T):
     return res
 
 
+def bench_bf16(args):
+    """The bf16-expert path on one layer of random bf16 experts (gate_up [E, H, 2, I], down
+    [E, I, H]): prefill = router -> mapping -> moe_cte(shard_on_block), GEMM durations from
+    the library's stage events in a pass of their own; decode = moe_block_tkg (RMSNorm,
+    router, experts), eager steps.  One JSON line."""
+    import torch
+
+    import pkgload
+
+    pkgload.load()
+    from vllm_neuron_amd import functional as NF
+
+    dev = torch.device("cuda:0")
+    E, K, H, I, limit, biases, dT, pT = WORKLOADS[args.workload]
+    dT = args.decode_tokens or dT
+    pT = args.prefill_tokens or pT
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    rn = lambda *s, std: (torch.randn(*s, device=dev, generator=g) * std).to(torch.bfloat16)  # noqa: E731
+    gu, dn = rn(E, H, 2, I, std=H ** -0.5), rn(E, I, H, std=I ** -0.5)
+    gb = rn(E, 2, I, std=0.02) if biases else None
+    db = rn(E, H, std=0.02) if biases else None
+    rw = rn(H, E, std=0.02)
+    lim = {} if limit is None else dict(gate_clamp_upper_limit=limit,
+                                        up_clamp_upper_limit=limit + 1,
+                                        up_clamp_lower_limit=-limit + 1)
+    act = "Swish" if limit is not None else "SiLU"
+
+    def timed(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        end = time.perf_counter() + args.settle
+        while time.perf_counter() < end:
+            fn()
+            torch.cuda.synchronize()
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    x = torch.randn(pT, H, device=dev, generator=g).to(torch.bfloat16)
+
+    def prefill(evs=None):
+        aff = NF.router(x, rw, K, None, "softmax", computation_dtype=torch.float32)
+        am, tp, b2e, _ = NF.build_blockwise_mapping(aff, E, K, 256)
+        return NF.moe_cte(x, am, gu, dn, tp, b2e, 256, implementation="shard_on_block",
+                          gate_and_up_proj_bias=gb, down_proj_bias=db, activation_function=act,
+                          stage_events=evs, **lim)
+
+    pms = timed(prefill, args.prefill_steps)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    stage = {"gate_up": [], "down": [], "combine": []}
+    for _ in range(args.prefill_steps):
+        prefill(evs)
+        torch.cuda.synchronize()
+        for i, k in enumerate(stage):
+            stage[k].append(evs[i].elapsed_time(evs[i + 1]))
+    med = {k: sorted(v)[len(v) // 2] for k, v in stage.items()}
+    pairs = pT * K
+    gu_tf = pairs * 4 * H * I / (med["gate_up"] * 1e-3) / 1e12
+    dn_tf = pairs * 2 * H * I / (med["down"] * 1e-3) / 1e12
+
+    xd = torch.randn(dT, H, device=dev, generator=g).to(torch.bfloat16)
+    gamma = torch.ones(1, H, device=dev)
+    dms = timed(lambda: NF.moe_block_tkg(
+        xd.unsqueeze(0), gamma, rw, gu, dn, top_k=K, expert_gate_up_bias=gb,
+        expert_down_bias=db, router_act_fn="SOFTMAX", router_pre_norm=False,
+        expert_affinities_scaling_mode="POST_SCALE", hidden_act_fn=act,
+        skip_router_logits=True, **lim), args.steps)
+    from vllm_neuron_amd.functional.moe.moe_block_tkg import rmsnorm
+    xn = rmsnorm(xd, gamma, 1e-6)
+    touched = int(torch.topk(xn.float() @ rw.float(), K, dim=1).indices.unique().numel())
+    dbytes = touched * 3 * H * I * 2
+    out = {
+        "metric": "bf16-expert MoE layer tokens/s @1 GPU (secondary path)",
+        "value": dT / (dms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": 0, "ms_per_step": dms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random bf16 experts, N(0,1) tokens), weights resident in HBM",
+        "config": {"workload": f"{args.workload}-shaped MoE layer, bf16 experts, decode {dT} "
+                               f"tokens", "experts": E, "top_k": K, "hidden": H,
+                   "intermediate": I, "weights": "bf16", "parallelism": "single GPU"},
+        "decode": {"ms_per_step": dms, "experts_touched": touched, "expert_bytes": dbytes,
+                   "GBps": dbytes / (dms * 1e-3) / 1e9,
+                   "frac_hbm": dbytes / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "prefill": {"tokens": pT, "ms_per_step": pms, "tokens_per_s": pT / (pms * 1e-3),
+                    "kernel_ms": med, "gate_up_TFLOPs": gu_tf, "down_TFLOPs": dn_tf,
+                    "gate_up_frac_bf16_peak": gu_tf / BF16_PEAK_TFLOPS,
+                    "expert_bytes": E * 3 * H * I * 2,
+                    "frac_hbm": E * 3 * H * I * 2 / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -216,6 +317,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.weights == "bf16":
+        bench_bf16(args)
         return
 
     import torch
