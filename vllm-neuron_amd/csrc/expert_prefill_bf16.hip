@@ -36,12 +36,15 @@
 namespace mxmoe {
 
 constexpr int kBN = 128;               // output columns per N-tile
-constexpr int kBK = 128;               // K per chunk
-constexpr int kBRow = kBK * 2;         // bytes of one LDS row (a slot's or a column's chunk)
+constexpr int kBK = 64;                // K per chunk
 constexpr int kBThreads = 256;
 constexpr int kBGateUpCols = kBN / 2;  // intermediate columns of a gate_up N-tile
-static_assert(kBThreads == 16 * 16, "one 8 x 8 weight block per thread and chunk");
-static_assert(kPM * (kBRow / 16) == 8 * kBThreads, "8 activation blocks per thread and chunk");
+constexpr int kBArow = kBK * 2;        // bytes of an activation row's chunk (8 blocks of 16 B)
+constexpr int kBWrow = kBN * 2;        // bytes of a weight row's chunk (128 columns)
+constexpr int kBAbytes = kPM * kBArow;                 // 16 KiB
+constexpr int kBStage = kBAbytes + kBK * kBWrow;       // + 16 KiB of weights
+static_assert(kPM * (kBArow / 16) == 4 * kBThreads, "4 activation blocks per thread and chunk");
+static_assert(kBK * (kBWrow / 16) == 4 * kBThreads, "4 weight blocks per thread and chunk");
 
 // The decode flow's extra operands (null in the prefill flow).
 struct Bf16Args {
@@ -51,87 +54,104 @@ struct Bf16Args {
   float* y32;            // down: y [slots, H] fp32
 };
 
-// LDS byte offset of 16-byte block `blk` (0..15) of row `row`.
-__device__ __forceinline__ uint32_t bsw(int row, int blk) {
-  return (uint32_t)row * kBRow + (uint32_t)((blk ^ (row & 15)) << 4);
+// Activation stage: row r (slot), 16-byte block b of its 64 K-values, XOR-swizzled so
+// that the 16 rows an operand read touches (two per 256-byte bank window) hit distinct banks.
+__device__ __forceinline__ uint32_t a_off(int r, int b) {
+  return (uint32_t)r * kBArow + (uint32_t)((b ^ ((r >> 1) & 7)) << 4);
+}
+// Weight stage: row k (K), column n of the N-tile, row-major as in memory; the 32-byte
+// groups of 16 columns are XOR-swizzled by k so that the 16 rows one transposing read
+// touches (k = 8 g + j and + 4, g, j = 0..3) spread over 8 distinct groups.
+__device__ __forceinline__ uint32_t w_swz(int k) { return (uint32_t)((k & 3) | (((k >> 3) & 1) << 2)); }
+__device__ __forceinline__ uint32_t w_off(int k, int n) {
+  return (uint32_t)kBAbytes + (uint32_t)k * kBWrow +
+         ((((uint32_t)(n >> 4)) ^ w_swz(k)) << 5) + (uint32_t)((n & 15) << 1);
 }
 
-// in[r] = 8 bf16 of row r (word w = columns 2w, 2w + 1) -> out[j] = 8 bf16 of column j
-// (word v = rows 2v, 2v + 1; the lower row in the low half).
-__device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint32_t a = in[2 * v][w], b = in[2 * v + 1][w];
-      out[2 * w][v] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // low halves
-      out[2 * w + 1][v] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // high halves
-    }
-}
-
-// One chunk's global -> register loads of a thread: 8 activation blocks (rows
-// tid / 16 + 16 i, block tid % 16) and an 8 x 8 weight block (rows 8 (tid / 16) ..,
-// columns of group tid % 16).  Past K, for columns past the projection and for slots
-// after the tile's last real one (padding: its outputs are never stored), zeros.
+// One chunk's global -> register loads of a thread: 4 activation blocks (rows tid / 8 +
+// 32 i, block tid % 8) and 4 weight blocks (rows tid / 16 + 16 j, columns 8 (tid % 16) ..).
+// Every load is issued, from a clamped address where its data is not used (past K, columns
+// past the projection, slots after the tile's last real one), and `valid` marks the blocks
+// to keep: the store writes zeros for the others.  Loads under a lane condition would make
+// the compiler wait for all outstanding loads where the paths meet.
 struct BChunk {
-  u32x4 a[8];
-  u32x4 w[8];
+  u32x4 a[4];
+  u32x4 w[4];
+  uint32_t valid;  // bit i: a[i]; bit 4 + j: w[j]
 };
 
-template <bool GATE_UP>
-__device__ __forceinline__ void bf16_load(BChunk& r, const char* abase, const uint32_t (&aoff)[8],
+__device__ __forceinline__ void bf16_load(BChunk& r, const char* abase, const uint32_t (&aoff)[4],
                                           const uint16_t* wsrc, bool wcol_ok, size_t ldw, int K,
                                           int kc, int last) {
   const int tid = threadIdx.x;
-  const int blk = tid & 15, kb = tid >> 4;
-  const u32x4 z = {0u, 0u, 0u, 0u};
-  const bool a_ok = kc + 8 * blk < K;  // K % 32 == 0: a block is whole or past K
+  const int ab = tid & 7, ar = tid >> 3, kr = tid >> 4;
+  const bool a_ok = kc + 8 * ab < K;  // K % 32 == 0: a block is whole or past K
+  uint32_t v = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    r.a[i] = (a_ok && kb + 16 * i <= last)
-                 ? *reinterpret_cast<const u32x4*>(abase + aoff[i] + (size_t)(kc + 8 * blk) * 2)
-                 : z;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int k = kc + 8 * kb + j;
-    r.w[j] = (wcol_ok && k < K) ? *reinterpret_cast<const u32x4*>(wsrc + (size_t)k * ldw) : z;
+  for (int i = 0; i < 4; ++i) {
+    const bool ok = a_ok && ar + 32 * i <= last;
+    v |= (uint32_t)ok << i;
+    r.a[i] = *reinterpret_cast<const u32x4*>(abase + aoff[i] + (ok ? (size_t)(kc + 8 * ab) * 2 : 0));
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k = kc + kr + 16 * j;
+    const bool ok = wcol_ok && k < K;
+    v |= (uint32_t)ok << (4 + j);
+    r.w[j] = *reinterpret_cast<const u32x4*>(wsrc + (ok ? (size_t)k * ldw : 0));
+  }
+  r.valid = v;
 }
 
-__device__ __forceinline__ void bf16_store_lds(const BChunk& r, uint8_t* sa, uint8_t* sw) {
+__device__ __forceinline__ void bf16_store_lds(const BChunk& r, uint8_t* st) {
   const int tid = threadIdx.x;
-  const int blk = tid & 15, kb = tid >> 4;
+  const int ab = tid & 7, ar = tid >> 3, nb = tid & 15, kr = tid >> 4;
+  const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *reinterpret_cast<u32x4*>(sa + bsw(kb + 16 * i, blk)) = r.a[i];
-  u32x4 t[8];
-  transpose8x8(r.w, t);
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<u32x4*>(st + a_off(ar + 32 * i, ab)) = (r.valid >> i) & 1 ? r.a[i] : z;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(sw + bsw(8 * blk + j, kb)) = t[j];
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<u32x4*>(st + w_off(kr + 16 * j, 8 * nb)) =
+        (r.valid >> (4 + j)) & 1 ? r.w[j] : z;
 }
 
-// One chunk's MFMAs of a wave: 4 K-steps of 32, each 4 weight and 4 activation operand
-// reads (lane l: row l % 16 of the tile, K-values 8 (l / 16) .. + 7 of the step).  All 4
-// subtiles run: skipping those past the tile's last real slot branched around each MFMA
-// and measured 15 % slower.
-__device__ __forceinline__ void bf16_compute(const uint8_t* sa, const uint8_t* sw, int fh, int sh,
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+// 4 K-values (rows k, k + 1, k + 2, k + 3 of column n + lane % 16) of the weight stage by
+// gfx950's transposing LDS read: in each 16-lane group, lane 4 j + q reads row k + j,
+// columns n + 4 q .. + 3, and lane i receives column n + i of the 4 rows.
+__device__ __forceinline__ s16x4 w_tr(const uint8_t* st, int k, int n) {
+  const int li = threadIdx.x & 15;
+  const uint8_t* p = st + w_off(k + (li >> 2), n + 4 * (li & 3));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)((__attribute__((address_space(3))) uint8_t*)p));
+}
+
+// One chunk's MFMAs of a wave: 2 K-steps of 32, each 4 weight operands (two transposing
+// reads each) and 4 activation operands (one 16-byte read each; lane l: row l % 16 of the
+// subtile, K-values 8 (l / 16) .. + 7 of the step).
+__device__ __forceinline__ void bf16_compute(const uint8_t* st, int fh, int sh,
                                              f32x4 (&acc)[4][4]) {
   const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
 #pragma unroll
   for (int ks = 0; ks < kBK / 32; ++ks) {
-    const int blk = 4 * ks + lq;
     bf16x8 wa[4], xb[4];
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
-      wa[f] = as_bf16x8(*reinterpret_cast<const u32x4*>(sw + bsw(64 * fh + 16 * f + li, blk)));
+    for (int f = 0; f < 4; ++f) {
+      const int k = 32 * ks + 8 * lq, n = 64 * fh + 16 * f;
+      const s16x4 lo = w_tr(st, k, n), hi = w_tr(st, k + 4, n);
+      const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      wa[f] = __builtin_bit_cast(bf16x8, v);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      xb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + bsw(64 * sh + 16 * s + li, blk)));
+      xb[s] = as_bf16x8(*reinterpret_cast<const u32x4*>(st + a_off(64 * sh + 16 * s + li,
+                                                                   4 * ks + lq)));
 #pragma unroll
     for (int f = 0; f < 4; ++f)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc[f][s] = mfma16(wa[f], xb[s], acc[f][s]);
+      for (int s = 0; s < 4; ++s) acc[f][s] = mfma16(wa[f], xb[s], acc[f][s]);
   }
 }
 
@@ -291,7 +311,7 @@ template <bool GATE_UP, bool F32>
 __global__ void __launch_bounds__(kBThreads)
     __attribute__((amdgpu_waves_per_eu(2, 2))) prefill_gemm_bf16_kernel(Bf16Args bargs) {
   const PrefillArgs& args = bargs.p;
-  __shared__ __attribute__((aligned(1024))) uint8_t s_a[kPM * kBRow], s_w[kBN * kBRow];
+  __shared__ __attribute__((aligned(1024))) uint8_t s_st[2][kBStage];
   __shared__ int32_t stok[kPM];
   __shared__ uint32_t s_rowoff[kPM];
   __shared__ int s_lastw[kPM / 64];
@@ -323,9 +343,9 @@ __global__ void __launch_bounds__(kBThreads)
     scol = wcol_ok ? n : 0;
   }
   const uint16_t* wbase = reinterpret_cast<const uint16_t*>(args.wq) + (size_t)e * K * ldw + scol;
-  uint32_t aoff[8];
+  uint32_t aoff[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) aoff[i] = s_rowoff[(tid >> 4) + 16 * i];
+  for (int i = 0; i < 4; ++i) aoff[i] = s_rowoff[(tid >> 3) + 32 * i];
   const char* abase = reinterpret_cast<const char*>(args.a);
 
   f32x4 acc[4][4];
@@ -338,24 +358,34 @@ __global__ void __launch_bounds__(kBThreads)
   constexpr bool TWO = F32 && !GATE_UP;
   const int ncc = TWO ? 2 * nc : nc;
   const char* abase_lo = TWO ? reinterpret_cast<const char*>(bargs.a_lo) : abase;
-  BChunk r;
-  bf16_load<GATE_UP>(r, abase, aoff, wbase, wcol_ok, ldw, K, 0, last);
-  bf16_store_lds(r, s_a, s_w);
+  auto load = [&](BChunk& r, int cc) {
+    cc = min(cc, ncc - 1);  // past the last chunk: a re-read that is never stored
+    const bool lo = TWO && cc >= nc;
+    bf16_load(r, lo ? abase_lo : abase, aoff, wbase, wcol_ok, ldw, K, (lo ? cc - nc : cc) * kBK,
+              last);
+  };
+  // Two LDS stages (chunk c in stage c % 2) and two register chunks: while chunk c's MFMAs
+  // run, the loads of chunks c + 1 and c + 2 are in flight; chunk c + 1 goes to LDS after
+  // them, and one barrier per chunk orders the stages.
+  // Every load is issued unconditionally, in a fixed order (chunks past the last re-read
+  // the last one): with loads on some paths only, the compiler could not count the loads
+  // still in flight and would wait for all of them before each store.
+  BChunk r0, r1;
+  load(r0, 0);
+  load(r1, 1);
+  bf16_store_lds(r0, s_st[0]);
+  load(r0, 2);
   __syncthreads();
-  for (int c = 0; c < ncc; ++c) {
-    const bool more = c + 1 < ncc;
-    if (more) {
-      const int cn = c + 1;
-      const bool lo = TWO && cn >= nc;
-      bf16_load<GATE_UP>(r, lo ? abase_lo : abase, aoff, wbase, wcol_ok, ldw, K,
-                         (lo ? cn - nc : cn) * kBK, last);
-    }
-    if (active) bf16_compute(s_a, s_w, fh, sh, acc);
+  // Stores past the last chunk write re-read data that no compute reads.
+  for (int c = 0; c < ncc; c += 2) {
+    if (active) bf16_compute(s_st[0], fh, sh, acc);
+    bf16_store_lds(r1, s_st[1]);
     __syncthreads();
-    if (more) {
-      bf16_store_lds(r, s_a, s_w);
-      __syncthreads();
-    }
+    load(r1, c + 3);
+    if (active && c + 1 < ncc) bf16_compute(s_st[1], fh, sh, acc);
+    bf16_store_lds(r0, s_st[0]);
+    __syncthreads();
+    load(r0, c + 4);
   }
   if (!active) return;
   if constexpr (F32) {
