@@ -69,51 +69,50 @@ __device__ __forceinline__ uint32_t w_off(int k, int n) {
 }
 
 // One chunk's global -> register loads of a thread: 4 activation blocks (rows tid / 8 +
-// 32 i, block tid % 8) and 4 weight blocks (rows tid / 16 + 16 j, columns 8 (tid % 16) ..).
-// Every load is issued, from a clamped address where its data is not used (past K, columns
-// past the projection, slots after the tile's last real one), and `valid` marks the blocks
-// to keep: the store writes zeros for the others.  Loads under a lane condition would make
-// the compiler wait for all outstanding loads where the paths meet.
+// 32 i, block tid % 8) and 4 weight blocks (rows tid / 16 + 16 j, columns 8 (tid % 16) ..),
+// as bounds-checked buffer loads: a block whose data is not wanted (past K, columns past
+// the projection, slots after the tile's last real one) gets an offset past the resource's
+// range, which returns zeros without a memory access.  Every load is issued, in a fixed
+// order: loads under a lane condition would make the compiler wait for all outstanding
+// loads where the paths meet.
 struct BChunk {
   u32x4 a[4];
   u32x4 w[4];
-  uint32_t valid;  // bit i: a[i]; bit 4 + j: w[j]
 };
+constexpr uint32_t kBOff = 0xFFFFFFF0u;  // past every resource's range (each is < 4 GiB, in 64-byte rows)
+// Raw buffer resource over [p, p + bytes): stride 0, the gfx9-family data format word.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bf16_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
-__device__ __forceinline__ void bf16_load(BChunk& r, const char* abase, const uint32_t (&aoff)[4],
-                                          const uint16_t* wsrc, bool wcol_ok, size_t ldw, int K,
-                                          int kc, int last) {
+__device__ __forceinline__ void bf16_load(BChunk& r, __amdgpu_buffer_rsrc_t ra,
+                                          const uint32_t (&aoff)[4], __amdgpu_buffer_rsrc_t rw,
+                                          uint32_t wcol, bool wcol_ok, uint32_t ldw, int K, int kc,
+                                          int last) {
   const int tid = threadIdx.x;
   const int ab = tid & 7, ar = tid >> 3, kr = tid >> 4;
   const bool a_ok = kc + 8 * ab < K;  // K % 32 == 0: a block is whole or past K
-  uint32_t v = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool ok = a_ok && ar + 32 * i <= last;
-    v |= (uint32_t)ok << i;
-    r.a[i] = *reinterpret_cast<const u32x4*>(abase + aoff[i] + (ok ? (size_t)(kc + 8 * ab) * 2 : 0));
+    const uint32_t o = ok ? aoff[i] + (uint32_t)(kc + 8 * ab) * 2u : kBOff;
+    r.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)o, 0, 0));
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int k = kc + kr + 16 * j;
-    const bool ok = wcol_ok && k < K;
-    v |= (uint32_t)ok << (4 + j);
-    r.w[j] = *reinterpret_cast<const u32x4*>(wsrc + (ok ? (size_t)k * ldw : 0));
+    const uint32_t o = (wcol_ok && k < K) ? ((uint32_t)k * ldw + wcol) * 2u : kBOff;
+    r.w[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)o, 0, 0));
   }
-  r.valid = v;
 }
 
 __device__ __forceinline__ void bf16_store_lds(const BChunk& r, uint8_t* st) {
   const int tid = threadIdx.x;
   const int ab = tid & 7, ar = tid >> 3, nb = tid & 15, kr = tid >> 4;
-  const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<u32x4*>(st + a_off(ar + 32 * i, ab)) = (r.valid >> i) & 1 ? r.a[i] : z;
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(st + a_off(ar + 32 * i, ab)) = r.a[i];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    *reinterpret_cast<u32x4*>(st + w_off(kr + 16 * j, 8 * nb)) =
-        (r.valid >> (4 + j)) & 1 ? r.w[j] : z;
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(st + w_off(kr + 16 * j, 8 * nb)) = r.w[j];
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -342,12 +341,16 @@ __global__ void __launch_bounds__(kBThreads)
     wcol_ok = n < args.H;
     scol = wcol_ok ? n : 0;
   }
-  const uint16_t* wbase = reinterpret_cast<const uint16_t*>(args.wq) + (size_t)e * K * ldw + scol;
+  // Buffer resources: this expert's weights (K rows of ldw), the activation rows (tokens,
+  // or slots when the rows are per slot) and, for the decode flow's down GEMM, the lo rows.
+  const __amdgpu_buffer_rsrc_t rw = bf16_rsrc(
+      reinterpret_cast<const uint16_t*>(args.wq) + (size_t)e * K * ldw, (uint32_t)(K * ldw * 2));
+  const uint32_t a_rows = (GATE_UP && !args.a_by_slot) ? (uint32_t)args.T
+                                                       : (uint32_t)args.n_mtiles * kPM;
+  const __amdgpu_buffer_rsrc_t ra = bf16_rsrc(args.a, a_rows * (uint32_t)K * 2u);
   uint32_t aoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) aoff[i] = s_rowoff[(tid >> 3) + 32 * i];
-  const char* abase = reinterpret_cast<const char*>(args.a);
-
   f32x4 acc[4][4];
 #pragma unroll
   for (int f = 0; f < 4; ++f)
@@ -357,12 +360,13 @@ __global__ void __launch_bounds__(kBThreads)
   // The decode flow's down GEMM runs its chunks twice: hi rows of h, then lo rows.
   constexpr bool TWO = F32 && !GATE_UP;
   const int ncc = TWO ? 2 * nc : nc;
-  const char* abase_lo = TWO ? reinterpret_cast<const char*>(bargs.a_lo) : abase;
+  const __amdgpu_buffer_rsrc_t ra_lo =
+      TWO ? bf16_rsrc(bargs.a_lo, a_rows * (uint32_t)K * 2u) : ra;
   auto load = [&](BChunk& r, int cc) {
     cc = min(cc, ncc - 1);  // past the last chunk: a re-read that is never stored
     const bool lo = TWO && cc >= nc;
-    bf16_load(r, lo ? abase_lo : abase, aoff, wbase, wcol_ok, ldw, K, (lo ? cc - nc : cc) * kBK,
-              last);
+    bf16_load(r, lo ? ra_lo : ra, aoff, rw, (uint32_t)scol, wcol_ok, (uint32_t)ldw, K,
+              (lo ? cc - nc : cc) * kBK, last);
   };
   // Two LDS stages (chunk c in stage c % 2) and two register chunks: while chunk c's MFMAs
   // run, the loads of chunks c + 1 and c + 2 are in flight; chunk c + 1 goes to LDS after
