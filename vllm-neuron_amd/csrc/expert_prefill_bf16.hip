@@ -4,21 +4,18 @@
 // schedule (tile order, XCD groups), slot tables and epilogues as the MX GEMMs, which
 // stream packed codes instead.
 //
-// Workgroup tile: 128 slots x 128 output columns over K in 128-wide chunks, 4 waves in a
+// Workgroup tile: 128 slots x 128 output columns over K in 64-wide chunks, 4 waves in a
 // 2 x 2 grid (wave w: slots 64 (w & 1) .. +63, columns 64 (w >> 1) .. +63), each wave
 // 4 x 4 MFMA 16x16x32 tiles.  The weights are the MFMA's A operand (rows = output
 // columns) and the slots' activations its B operand, so a lane ends with 4 consecutive
-// output columns of one slot (one 8-byte store).  Both operands pass through LDS, one
-// chunk at a time:
-//   activations: 128 rows x 256 B, 16-byte blocks XOR-swizzled by row (the 16 rows an
-//     operand read touches then hit distinct banks);
-//   weights: transposed, [column][k] (256 B per column, the same swizzle), so a lane's
-//     8 K-values of a column are one 16-byte LDS read.  A thread loads an 8 (k) x 8
-//     (column) block with 8 row loads of 16 B (16 lanes read 256 contiguous bytes of a
-//     row), transposes it in registers with byte permutes and writes 8 columns of 16 B.
-// The next chunk's global loads are issued before the current chunk's MFMAs and land in
-// registers while they run; LDS is refilled between two barriers.  64 KiB of LDS per
-// workgroup: two workgroups per CU.
+// output columns of one slot (one 8-byte store).  Both operands pass through LDS, in two
+// stages of one chunk each (32 KiB: 64 KiB per workgroup, two workgroups per CU):
+//   activations: 128 rows x 128 B, 16-byte blocks XOR-swizzled by row pair;
+//   weights: row-major as in memory (64 rows x 256 B), 32-byte column groups XOR-swizzled
+//     by row; a lane's 8 K-values of one column come from two transposing LDS reads
+//     (ds_read_b64_tr_b16).
+// Global -> register loads are bounds-checked buffer loads issued in a fixed order, two
+// chunks ahead of the MFMAs; one barrier per chunk orders the stages.
 // gate_up N-tile: 64 intermediate columns as 4 pairs of 16-column tiles (gate, up) so
 // that a lane holds gate and up of the same columns; down N-tile: 128 columns of H.
 // Two flows share the GEMMs (template F32):
