@@ -35,6 +35,7 @@ CASES = [
     (6, 2, 416, 288, 77, 128, "SiLU", False, True),    # K and N tails in both GEMMs
     (4, 1, 96, 64, 129, 512, "GELU", False, False),
     (3, 3, 128, 96, 1, 128, "Swish", True, True),      # one token
+    (2, 1, 32, 32, 5, 128, "SiLU", False, True),       # smallest K and N: one partial chunk
 ]
 
 
@@ -209,6 +210,7 @@ def test_moe_tkg_rejects_bf16_weights(dev):
     (1, 16, 4, 512, 384, "SOFTMAX", False, "POST_SCALE"),
     (7, 8, 2, 416, 288, "SIGMOID", True, "NO_SCALE"),       # K and N tails in both GEMMs
     (64, 16, 4, 512, 384, "SOFTMAX", False, "POST_SCALE"),
+    (3, 4, 2, 32, 32, "SOFTMAX", False, "POST_SCALE"),       # smallest K and N
 ])
 def test_moe_block_tkg_bf16_weights(dev, T, E, k, H, I, act, pre_norm, scale):
     """moe_block_tkg with bf16 experts against the oracle's dense torch flow
