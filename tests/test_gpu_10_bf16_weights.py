@@ -286,3 +286,73 @@ def test_bf16_model_decode_call(dev):
     got = out.cpu()
     assert got.shape == (T, H)
     check_close(got.float(), want.float(), None, "bf16 model decode call")
+
+
+def _device_experts(dev, seed, E, H, I):
+    """bf16 experts drawn on the GPU one expert at a time (gate_up [E, H, 2, I], down [E, I, H],
+    biases [E, 2, I] / [E, H]): the 120B-shaped set is 6.4 GB."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    gu = torch.empty(E, H, 2, I, dtype=torch.bfloat16, device=dev)
+    dn = torch.empty(E, I, H, dtype=torch.bfloat16, device=dev)
+    for e in range(E):
+        gu[e] = (torch.randn(H, 2, I, device=dev, generator=g) * H ** -0.5).to(torch.bfloat16)
+        dn[e] = (torch.randn(I, H, device=dev, generator=g) * I ** -0.5).to(torch.bfloat16)
+    gb = (torch.randn(E, 2, I, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    db = (torch.randn(E, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    return gu, dn, gb, db
+
+
+def _subset(aff_rows, *tensors):
+    """The experts the sampled rows select, ascending (the order the flows sum them in):
+    affinities [rows, E_sub] and each [E, ...] tensor restricted to them, on the CPU."""
+    sel = torch.nonzero((aff_rows != 0).any(0)).flatten()
+    return (aff_rows[:, sel],) + tuple(t[sel.to(t.device)].cpu() for t in tensors)
+
+
+def test_bf16_weights_gptoss120b_shape(dev):
+    """120B-shaped layer with bf16 experts (E=128, top-4, H = I = 2880, clamped Swish):
+    decode of 64 tokens through moe_block_tkg and prefill of 2,048 tokens through moe_cte,
+    sampled rows against the oracle's flows over the experts those rows select."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    from oracle import blockwise as ob
+    from oracle import moe_block_tkg as obt
+    from oracle import moe_cte as oc
+
+    E, k, H, I = 128, 4, 2880, 2880
+    lim = dict(gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0, up_clamp_lower_limit=-6.0)
+    gu, dn, gb, db = _device_experts(dev, 140, E, H, I)
+    rw = synthetic.normal_bf16(141, (H, E), 0.05)
+
+    # decode
+    T = 64
+    x = synthetic.tokens(142, T, H)
+    gamma = torch.ones(H)
+    out = NF.moe_block_tkg(x.unsqueeze(0).to(dev), gamma.unsqueeze(0).to(dev), rw.to(dev), gu,
+                           dn, top_k=k, expert_gate_up_bias=gb, expert_down_bias=db,
+                           router_act_fn="SOFTMAX", router_pre_norm=False,
+                           expert_affinities_scaling_mode="POST_SCALE", hidden_act_fn="Swish",
+                           skip_router_logits=True, **lim).cpu()
+    rows = torch.arange(0, T, 9)
+    xn, _, top, idx = obt.rmsnorm_router(x, gamma, rw, None, 1e-6, k, "SOFTMAX", False, False)
+    aff = torch.zeros(T, E).scatter_(1, idx, top)[rows]
+    a_sub, gu_s, dn_s, gb_s, db_s = _subset(aff, gu, dn, gb, db)
+    want = obt.expert_mlp_fp32_routed(xn[rows], a_sub, gu_s, dn_s, gb_s, db_s,
+                                      hidden_act_fn="Swish", scale_mode="POST_SCALE",
+                                      out_dtype=torch.bfloat16, **lim)
+    check_close(out[rows].float(), want.float(), None, "bf16 experts 120b decode")
+
+    # prefill
+    T = 2048
+    x = synthetic.tokens(143, T, H)
+    aff = _route(144, T, E, k)
+    am_g, tp, b2e, _ = NF.build_blockwise_mapping(aff.to(dev), E, k, 256)
+    got = NF.moe_cte(x.to(dev), am_g, gu, dn, tp, b2e, 256, implementation="shard_on_block",
+                     gate_and_up_proj_bias=gb, down_proj_bias=db, activation_function="Swish",
+                     **lim).cpu()
+    rows = torch.arange(0, T, 101)
+    a_sub, gu_s, dn_s, gb_s, db_s = _subset(aff[rows], gu, dn, gb, db)
+    want = oc.torch_moe_impl_routed(x[rows], a_sub.reshape(-1, 1), gu_s, dn_s, gb_s,
+                                    db_s.unsqueeze(1), activation_function="Swish", **lim)
+    check_close(got[rows].float(), want, None, "bf16 experts 120b prefill")
