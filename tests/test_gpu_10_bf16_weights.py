@@ -356,3 +356,43 @@ def test_bf16_weights_gptoss120b_shape(dev):
     want = oc.torch_moe_impl_routed(x[rows], a_sub.reshape(-1, 1), gu_s, dn_s, gb_s,
                                     db_s.unsqueeze(1), activation_function="Swish", **lim)
     check_close(got[rows].float(), want, None, "bf16 experts 120b prefill")
+
+
+def test_moe_block_tkg_bf16_weights_graph_replays(dev):
+    """The bf16-expert decode block (RMSNorm, router, scatter, mapping, both GEMMs, combine)
+    captured in a HIP graph after one eager call: every replay, with eager work and
+    synchronizations between them, equals the eager result for its input."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    E, k, H, I, T = 16, 4, 512, 384, 32
+    gu, dn, gb, db = (t.to(dev) for t in _bf16_experts(150, E, H, I))
+    rw = synthetic.normal_bf16(151, (H, E), 0.05).to(dev)
+    gamma = torch.ones(1, H, device=dev)
+    run = lambda x: NF.moe_block_tkg(  # noqa: E731
+        x.unsqueeze(0), gamma, rw, gu.reshape(E, H, 2, I), dn, top_k=k,
+        expert_gate_up_bias=gb.reshape(E, 2, I), expert_down_bias=db, router_act_fn="SOFTMAX",
+        router_pre_norm=False, expert_affinities_scaling_mode="POST_SCALE",
+        hidden_act_fn="Swish", skip_router_logits=True, gate_clamp_upper_limit=7.0)
+    xs = [synthetic.tokens(152 + i, T, H).to(dev) for i in range(3)]
+    eager = [run(x).clone() for x in xs]
+    torch.cuda.synchronize()
+    static_x = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(static_x)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out = run(static_x)
+    for rep in range(2):
+        for i, x in enumerate(xs):
+            static_x.copy_(x)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager[i]), (rep, i)
+            other = run(xs[(i + 1) % 3])  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(other, eager[(i + 1) % 3])
