@@ -58,6 +58,16 @@ int router_run(const RouterSpec& r, int64_t T, int64_t H, int64_t E, int top_k, 
 int rmsnorm_run(const uint16_t* x, const float* gamma, int64_t T, int64_t H, int64_t ha,
                 int all_cols, float eps, int out_dt, uint16_t* out, hipStream_t s);
 
+// Decode with bf16 expert weights by streaming items (expert_decode.hip): the routing,
+// tiles, activation and combine of the MXFP4 decode, for batches whose experts hold few
+// 16-token tiles.
+size_t tkg_bf16_stream_workspace(int64_t T, int64_t H, int64_t I, int64_t E, int K);
+int tkg_bf16_stream(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
+                    const uint16_t* gu_w, const uint16_t* dn_w, const uint16_t* gu_bias,
+                    const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
+                    int top_k, int act, const float* clamps, int scale_mode, uint16_t* out,
+                    void* workspace, size_t workspace_bytes, hipStream_t s);
+
 // Blocks of the blockwise mapping of T tokens with top_k experts each over E experts at
 // block size B: the reference's bound (moe_blockwise.py:343-349), at most one block per
 // routed slot.

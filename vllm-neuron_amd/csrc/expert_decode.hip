@@ -462,6 +462,7 @@ __device__ __forceinline__ void stream_tile(const StreamGeom& g, const char* b1,
 
 struct TkgArgs {
   const uint16_t* x;       // gate_up: tokens [T, H]
+  int T, S;                // tokens, routed slots (bounds of x and of h)
   const uint16_t* h_hi;    // down: activations [slots, I] (hi, lo)
   const uint16_t* h_lo;
   const uint8_t* wq;
@@ -933,6 +934,262 @@ static size_t decode_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t
   r.tkg = cv.take<char>(r.tkg_bytes);
   if (d) *d = r;
   return cv.off + 256;
+}
+
+// ---------------------------------------------------------------------------------------
+// Decode with bf16 expert weights (the bf16 model's moe_block_tkg operands: gate_up
+// [E][H][2I], each row gate columns then up columns; down [E][I][H]).  The routing, the
+// 16-token tiles, the split-K activation kernel and the combine are the MXFP4 decode's; the
+// streaming items differ: one wave per (tile, 64 output columns, K part), weights K-major.
+// Per 32-row chunk a lane loads 4 x 16 B of the weight block (8 lanes per 128-byte row
+// segment) and 16 B of its token's activations, bounds-checked buffer loads three chunks
+// ahead; the wave writes the block to its own 4 KiB of LDS and reads it back with the
+// transposing read (ds_read_b64_tr_b16) as MFMA A operands (rows = output columns, 8
+// K-values of one column per lane), the activations being the B operand (columns =
+// tokens).  No barrier: each wave only reads what it wrote, and its LDS operations run in
+// order.  gate_up writes raw K-part sums [nq, S, 2I] (tkg_act_kernel adds the parts, bias,
+// clamps and activation); down reads h as hi + lo (two MFMAs, exact bf16 products) and
+// writes its K parts [nq, S, H], the first carrying the bias (tkg_combine_kernel adds them).
+constexpr int kBdCols = 64;    // output columns per item
+constexpr int kBdK = 32;       // K rows per chunk
+constexpr int kBdWaves = 4;    // waves per workgroup, each with its own LDS block
+constexpr int kBdBlock = kBdK * kBdCols * 2;  // 4 KiB
+constexpr uint32_t kBdOff = 0xFFFFFFF0u;      // past every buffer resource's range
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bd_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bd_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+// LDS byte offset of (row r, column c) in a wave's [32][64] bf16 block: 32-byte column groups
+// XOR-swizzled by row so that the 16 rows one transposing read touches spread over the banks.
+__device__ __forceinline__ uint32_t bd_off(int r, int c) {
+  const uint32_t sw = (uint32_t)((((r >> 1) ^ (r >> 3)) & 3) << 1);
+  return (uint32_t)r * (kBdCols * 2) + ((((uint32_t)c >> 3) ^ sw) << 4) + (uint32_t)((c & 7) << 1);
+}
+typedef short bd_s16x4 __attribute__((ext_vector_type(4)));
+typedef short bd_s16x8 __attribute__((ext_vector_type(8)));
+
+struct BdChunk {
+  u32x4 w[4];
+  u32x4 x, x2;  // the lane's token's 8 K-values (down: hi, lo)
+};
+
+template <bool GATE_UP>
+__global__ void __launch_bounds__(64 * kBdWaves) __attribute__((amdgpu_waves_per_eu(3)))
+    tkgb_stream_kernel(TkgArgs a, float* __restrict__ out, size_t out_stride) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kBdWaves][kBdBlock];
+  const int N = GATE_UP ? 2 * a.I : a.H;  // output columns = weight row length
+  const int K = GATE_UP ? a.H : a.I;
+  const int nb = (N + kBdCols - 1) / kBdCols;
+  const int wave = wave_id();
+  const int u = blockIdx.x * kBdWaves + wave;
+  if (u >= *a.n_tiles * nb * a.nq) return;
+  const int item = u / a.nq, q = u - item * a.nq;
+  const int ti = item / nb, cb = (item - ti * nb) * kBdCols;
+  const int4 tm = reinterpret_cast<const int4*>(a.tiles)[ti];
+  const int e = __builtin_amdgcn_readfirstlane(tm.x);
+  const int s0 = __builtin_amdgcn_readfirstlane(tm.y);
+  const int ne = __builtin_amdgcn_readfirstlane(tm.z);
+  const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
+  const int nc = K / kBdK;
+  const int c0 = q * a.cpq, c1 = min(nc, c0 + a.cpq);
+  // weights of expert e, K rows of N; this lane's 16-byte block: row lane / 8 + 8 j, columns
+  // cb + 8 (lane % 8) ..
+  const __amdgpu_buffer_rsrc_t rw = bd_rsrc(
+      reinterpret_cast<const uint16_t*>(a.wq) + (size_t)e * K * N, (uint32_t)((size_t)K * N * 2));
+  const int wc = cb + 8 * (lane & 7), wr = lane >> 3;
+  const bool wc_ok = wc < N;
+  // activations: gate_up x[token] of [T, H]; down h rows [slots, I] (hi, lo)
+  const bool t_ok = li < ne;
+  uint32_t xrow = 0;
+  if (t_ok) xrow = GATE_UP ? (uint32_t)a.slot_tok[s0 + li] : (uint32_t)(s0 + li);
+  const uint32_t x_rows = GATE_UP ? (uint32_t)a.T : (uint32_t)a.S;
+  const __amdgpu_buffer_rsrc_t rx =
+      bd_rsrc(GATE_UP ? (const void*)a.x : (const void*)a.h_hi, x_rows * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rx2 =
+      bd_rsrc(GATE_UP ? (const void*)a.x : (const void*)a.h_lo, x_rows * (uint32_t)K * 2u);
+  auto load = [&](BdChunk& f, int c) {
+    c = min(c, c1 - 1);  // past the part's last chunk: a re-read that is never used
+    const int kc = c * kBdK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.w[j] = bd_load(rw, wc_ok ? ((uint32_t)(kc + wr + 8 * j) * (uint32_t)N + (uint32_t)wc) * 2u
+                                 : kBdOff);
+    const uint32_t xo = t_ok ? (xrow * (uint32_t)K + (uint32_t)(kc + 8 * lq)) * 2u : kBdOff;
+    f.x = bd_load(rx, xo);
+    if (!GATE_UP) f.x2 = bd_load(rx2, xo);
+  };
+  uint8_t* blk = lds[wave];
+  f32x4 acc[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](const BdChunk& f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(blk + bd_off(wr + 8 * j, 8 * (lane & 7))) = f.w[j];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int n = 16 * t + 4 * (li & 3);
+      const int r = 8 * lq + (li >> 2);
+      const bd_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) bd_s16x4*)(
+              (__attribute__((address_space(3))) uint8_t*)(blk + bd_off(r, n))));
+      const bd_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) bd_s16x4*)(
+              (__attribute__((address_space(3))) uint8_t*)(blk + bd_off(r + 4, n))));
+      const bd_s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const bf16x8 wa = __builtin_bit_cast(bf16x8, v);
+      acc[t] = mfma16(wa, as_bf16x8(f.x), acc[t]);
+      if (!GATE_UP) acc[t] = mfma16(wa, as_bf16x8(f.x2), acc[t]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // three chunks in flight; every load issued in a fixed order (counted waits)
+  BdChunk r0, r1, r2;
+  load(r0, c0);
+  load(r1, c0 + 1);
+  load(r2, c0 + 2);
+  // No exit inside the loop: the steps past the part's last chunk are skipped, their loads
+  // still issued, so every path issues the same loads and the waits stay counted.
+  for (int c = c0; c < c1; c += 3) {
+    step(r0);
+    load(r0, c + 3);
+    if (c + 1 < c1) step(r1);
+    load(r1, c + 4);
+    if (c + 2 < c1) step(r2);
+    load(r2, c + 5);
+  }
+  if (!t_ok) return;
+  const size_t slot = (size_t)(s0 + li);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int n = cb + 16 * t + 4 * lq;
+    if (n >= N) continue;
+    f32x4 v = acc[t];
+    if (!GATE_UP && a.bias && q == 0) {  // the first K part carries the down bias
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += bf16_bits_to_f32(a.bias[(size_t)e * N + n + i]);
+    }
+    *reinterpret_cast<f32x4*>(out + q * out_stride + slot * N + n) = v;
+  }
+}
+
+// K parts of the bf16 items: enough units for the wave slots (about 3,000), at most 8 parts.
+static void tkgb_parts(double units, int nc, int& nq, int& cpq) {
+  int q = (int)ceil(3000.0 / (units > 1.0 ? units : 1.0));
+  tkg_parts(nc, q > 8 ? 8 : q, nq, cpq);
+}
+
+struct TkgbPlan {
+  int nq_gu, cpq_gu, nq_dn, cpq_dn;
+};
+static TkgbPlan tkgb_plan(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
+  const double active = (double)E * (1.0 - pow(1.0 - (double)K / (double)E, (double)T));
+  const double tiles = active + ((double)(T * K) - active) / 16.0;
+  TkgbPlan p;
+  tkgb_parts(tiles * (double)((2 * I + kBdCols - 1) / kBdCols), (int)(H / kBdK), p.nq_gu,
+             p.cpq_gu);
+  tkgb_parts(tiles * (double)((H + kBdCols - 1) / kBdCols), (int)(I / kBdK), p.nq_dn, p.cpq_dn);
+  return p;
+}
+
+static size_t tkgb_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, int64_t E,
+                         int K, TkgWs* w) {
+  Carver cv(base, cap);
+  const int64_t S = T * K;
+  const TkgbPlan p = tkgb_plan(T, H, I, E, K);
+  TkgWs t;
+  t.expert_off = cv.take<int32_t>(E + 1);
+  t.active = cv.take<int32_t>(E);
+  t.n_active = cv.take<int32_t>(1);
+  t.slot_tok = cv.take<int32_t>(S);
+  t.tok_slot = cv.take<int32_t>(S);
+  t.tok_w = cv.take<float>(S);
+  t.tiles = cv.take<int32_t>(4 * tkg_max_tiles(T, E, K));
+  t.n_tiles = cv.take<int32_t>(1);
+  t.h_hi = cv.take<uint16_t>(S * I);
+  t.h_lo = cv.take<uint16_t>(S * I);
+  t.y = cv.take<float>(p.nq_dn * S * H);
+  t.part = cv.take<float>(p.nq_gu * S * 2 * I);
+  if (w) *w = t;
+  return cv.off + 256;
+}
+
+size_t tkg_bf16_stream_workspace(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
+  return tkgb_carve(nullptr, ~(size_t)0, T, H, I, E, K, nullptr);
+}
+
+// route -> gate_up items -> activation -> down items -> combine (bf16 expert weights).
+int tkg_bf16_stream(const uint16_t* x, const int32_t* topk_idx, const float* topk_val,
+                    const uint16_t* gu_w, const uint16_t* dn_w, const uint16_t* gu_bias,
+                    const uint16_t* dn_bias, int64_t T, int64_t H, int64_t I, int64_t E,
+                    int top_k, int act, const float* clamps, int scale_mode, uint16_t* out,
+                    void* workspace, size_t workspace_bytes, hipStream_t s) {
+  MXMOE_REQUIRE(T <= kTkgMaxT && E <= kTkgMaxE && top_k <= 8,
+                "moe_tkg_bf16: T=%lld, E=%lld or top_k=%d beyond the decode routing",
+                (long long)T, (long long)E, top_k);
+  const size_t need = tkgb_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
+  if (workspace_bytes < need)
+    return set_error(MXMOE_E_WORKSPACE, "moe_tkg_bf16: workspace %zu < %zu", workspace_bytes,
+                     need);
+  TkgWs w;
+  tkgb_carve(workspace, workspace_bytes, T, H, I, E, top_k, &w);
+  const TkgbPlan pl = tkgb_plan(T, H, I, E, top_k);
+  const int S = (int)(T * top_k);
+  TkgArgs a = {};
+  a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
+  a.p.gate_hi = clamps ? clamps[1] : INFINITY;
+  a.p.up_lo = clamps ? clamps[2] : -INFINITY;
+  a.p.up_hi = clamps ? clamps[3] : INFINITY;
+  a.p.act = act;
+  a.H = (int)H;
+  a.I = (int)I;
+  a.T = (int)T;
+  a.S = S;
+  a.expert_off = w.expert_off;
+  a.active = w.active;
+  a.n_active = w.n_active;
+  a.slot_tok = w.slot_tok;
+  a.tiles = w.tiles;
+  a.n_tiles = w.n_tiles;
+  hipLaunchKernelGGL(tkg_route_kernel, dim3(1), dim3(1024), 0, s, topk_idx, topk_val, (int)T,
+                     top_k, (int)E, scale_mode, w.expert_off, w.active, w.n_active, w.slot_tok,
+                     w.tok_slot, w.tok_w, w.tiles, w.n_tiles);
+  const int64_t n_tile_max = tkg_max_tiles(T, E, top_k);
+  auto blocks = [&](int64_t cols, int nq) {
+    const int64_t units = n_tile_max * ((cols + kBdCols - 1) / kBdCols) * nq;
+    return dim3((unsigned)((units + kBdWaves - 1) / kBdWaves));
+  };
+  TkgArgs gu = a;
+  gu.x = x;
+  gu.wq = reinterpret_cast<const uint8_t*>(gu_w);
+  gu.bias = gu_bias;
+  gu.nq = pl.nq_gu;
+  gu.cpq = pl.cpq_gu;
+  gu.part = w.part;
+  gu.part_stride = (size_t)S * 2 * (size_t)I;
+  gu.out_hi = w.h_hi;
+  gu.out_lo = w.h_lo;
+  hipLaunchKernelGGL(tkgb_stream_kernel<true>, blocks(2 * I, pl.nq_gu), dim3(64 * kBdWaves), 0,
+                     s, gu, w.part, gu.part_stride);
+  hipLaunchKernelGGL(tkg_act_kernel, dim3((unsigned)((I + 1023) / 1024), (unsigned)S),
+                     dim3(256), 0, s, gu, (int)E);
+  TkgArgs dn = a;
+  dn.h_hi = w.h_hi;
+  dn.h_lo = w.h_lo;
+  dn.wq = reinterpret_cast<const uint8_t*>(dn_w);
+  dn.bias = dn_bias;
+  dn.nq = pl.nq_dn;
+  dn.cpq = pl.cpq_dn;
+  dn.part_stride = (size_t)S * (size_t)H;
+  hipLaunchKernelGGL(tkgb_stream_kernel<false>, blocks(H, pl.nq_dn), dim3(64 * kBdWaves), 0, s,
+                     dn, w.y, dn.part_stride);
+  hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
+                     dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, pl.nq_dn,
+                     dn.part_stride, out);
+  return check_launch("moe_tkg_bf16");
 }
 
 }  // namespace mxmoe

@@ -1100,9 +1100,16 @@ static size_t tkg_bf16_carve(void* base, size_t cap, int64_t T, int64_t H, int64
 
 using namespace mxmoe;
 
+// Batches whose experts hold few 16-token tiles (the MXFP4 decode's one-tile rule) stream
+// the weights item by item (tkg_bf16_stream); larger ones run the blockwise GEMMs.
+static bool tkg_bf16_streams(int64_t T, int64_t E, int top_k) {
+  return (T <= 16 || T * top_k <= 8 * E) && T <= 1024 && E <= 512 && top_k <= 8;
+}
+
 extern "C" size_t mxmoe_moe_tkg_bf16_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E,
                                                      int top_k) {
   if (T < 1 || E < 1 || top_k < 1) return 256;
+  if (tkg_bf16_streams(T, E, top_k)) return tkg_bf16_stream_workspace(T, H, I, E, top_k);
   return tkg_bf16_carve(nullptr, ~(size_t)0, T, H, I, E, top_k, nullptr);
 }
 
@@ -1126,6 +1133,10 @@ extern "C" int mxmoe_moe_tkg_bf16(const uint16_t* x, const int32_t* topk_idx,
                 "moe_tkg_bf16: unsupported scale mode %d", scale_mode);
   MXMOE_REQUIRE((uintptr_t)gu_w % 16 == 0 && (uintptr_t)dn_w % 16 == 0,
                 "moe_tkg_bf16: bf16 weights must be 16-byte aligned");
+  if (tkg_bf16_streams(T, E, top_k))
+    return tkg_bf16_stream(x, topk_idx, topk_val, gu_w, dn_w, gu_bias, dn_bias, T, H, I, E, top_k,
+                           act, clamps, scale_mode, out, workspace, workspace_bytes,
+                           as_stream(stream));
   const int64_t n_slots = blockwise_n_blocks(T, E, top_k, kTkgBf16Block) * kTkgBf16Block;
   const int64_t kmax = H > I ? H : I;
   MXMOE_REQUIRE(n_slots / kPM <= kOrderMaxTiles && n_slots * kmax * 2 < ((int64_t)1 << 32) &&
