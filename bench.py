@@ -11,7 +11,9 @@ in [120, 130]), bf16 biases and router N(0, 0.02), tokens N(0, 1), clamped SwiGL
 Synthetic data: weights are drawn on the GPU directly in the packed layout (uniform
 random bytes are uniform codes in any byte order) for ``--layers`` distinct layers
 that the steps rotate through, so a step never finds its weights in the 256 MB
-last-level cache.  Inputs are resident in HBM before timing starts.
+last-level cache.  The GPT-OSS-120B-shaped workload holds all 36 MoE layers of that
+model by default (its whole expert set, 61 GB, resident on the GPU); the others 8.
+Inputs are resident in HBM before timing starts.
 
 Per-kernel durations come from HIP events the library records on the launch stream
 around each stage, in an eager pass of their own; the timed regions record none.  ``roofline`` covers the dominant kernel of
@@ -63,7 +65,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--workload", default="gptoss120b", choices=sorted(WORKLOADS))
-    ap.add_argument("--layers", type=int, default=8, help="distinct layers rotated")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="distinct layers rotated (default: 36 for gptoss120b, 8 otherwise)")
     ap.add_argument("--decode-tokens", type=int, default=None)
     ap.add_argument("--prefill-tokens", type=int, default=None)
     ap.add_argument("--skip-prefill", action="store_true")
@@ -330,7 +333,8 @@ def main():
     pT = args.prefill_tokens or pT
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    layers = [make_layer(E, K, H, I, limit, biases, dev, gen, args.zipf) for _ in range(args.layers)]
+    n_layers = args.layers or (36 if args.workload == "gptoss120b" else 8)
+    layers = [make_layer(E, K, H, I, limit, biases, dev, gen, args.zipf) for _ in range(n_layers)]
     L = len(layers)
     xs = [torch.randn(dT, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(L)]
     torch.cuda.synchronize()
@@ -380,9 +384,10 @@ def main():
     steps = args.steps
     mode = "eager"
     if not args.no_graph:
-        # One graph holds G consecutive steps (each layer G / L times); the timed region
-        # replays it, so ``steps`` is rounded to a multiple of G.
-        G = min(steps, 5 * L)
+        # One graph holds G consecutive steps over the rotated layers (a layer recurs at
+        # least 4 steps later, across replays); the timed region replays it, so ``steps``
+        # is rounded to a multiple of G.
+        G = min(steps, 40)
         reps = max(1, steps // G)
         steps = G * reps
         try:
