@@ -7,7 +7,8 @@
 //   route      one workgroup: per-expert slot lists (tokens ascending inside an
 //              expert), the list of active experts, per-token slots sorted by expert
 //   gate_up    streaming kernel, one wave per item (active expert, 4 row groups =
-//              2 gate/up pairs): the item's packed weights stream over all of K
+//              2 gate/up pairs; one pair in the smallest batches): the item's packed
+//              weights stream over all of K
 //              through a register ring of D chunks; fused bias, clamps and
 //              activation; the fp32 activation is stored as a bf16 (hi, lo) pair
 //   down       the same streaming kernel over (active expert, 4 row groups of H, or 8
@@ -344,9 +345,9 @@ __device__ __forceinline__ float act_f32(float g, int act) {
 // lane; with SPLIT a second (lo) copy).
 template <int R, int NT, bool SPLIT>
 struct ChunkFrag {
-  static_assert(R % 4 == 0, "a streamed tile is whole quads of row groups");
+  static_assert(R % 4 == 0 || R == 2, "a streamed tile is whole quads of row groups or a pair");
   u32x4 w[R];
-  uint32_t s[R / 4];
+  uint32_t s[(R + 3) / 4];
   u32x4 b[NT][4];
   u32x4 b2[SPLIT ? NT : 1][4];
 };
@@ -358,6 +359,7 @@ struct StreamGeom {
   int rv;             // valid row groups in the tile (<= R)
   int nfull, tail_q;  // full 128-wide chunks, 32-blocks in the partial last chunk
   int cb, ce;         // the K chunks [cb, ce) this tile streams
+  int sb;             // byte of the tile's first row group in its quad's scale word
 };
 
 // Plain loads only, so nothing waits on them before their use: lanes past K in a
@@ -384,7 +386,7 @@ __device__ __forceinline__ void load_chunk(ChunkFrag<R, NT, SPLIT>& f, int c, co
     f.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g.wq + off));
   }
 #pragma unroll
-  for (int h = 0; h < R / 4; ++h) {
+  for (int h = 0; h < (R + 3) / 4; ++h) {
     const uint32_t qq = 4 * h < g.rv ? h : 0;  // a partial last tile stays in its expert
     // Scales are read once per step too (non-temporal, about 2 % faster than cached).
     f.s[h] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
@@ -412,7 +414,11 @@ __device__ __forceinline__ void mma_chunk(const ChunkFrag<R, NT, SPLIT>& f, int 
       c < g.ce && ((c < g.nfull) || (c == g.nfull && ((threadIdx.x & 63) >> 4) < g.tail_q));
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const float sc = ok ? e8m0_to_f32((f.s[r / 4] >> (8 * (r % 4))) & 0xffu) : 0.0f;
+    // a pair (R = 2) sits in one quad, from byte g.sb (0 or 2) of its scale word;
+    // constant word indices keep the chunk in registers
+    const uint32_t sw = f.s[R % 4 == 0 ? r / 4 : 0];
+    const int sh = 8 * (R % 4 == 0 ? r % 4 : g.sb + r);
+    const float sc = ok ? e8m0_to_f32((sw >> sh) & 0xffu) : 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 wf = dequant8(f.w[r][j], sc);
@@ -524,6 +530,7 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
   g.wq = a.wq + ((size_t)e * n_rg + rg0) * (size_t)g.rg_bytes;
   g.ws = a.ws + ((size_t)e * ((n_rg + 3) / 4) + rg0 / 4) * (size_t)(2 * K);
   g.rv = min(R, n_rg - rg0);
+  g.sb = rg0 % 4;
   const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
                            : reinterpret_cast<const char*>(a.h_hi);
   const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
@@ -712,6 +719,13 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // (~965 items) 110.2 -> 103.5 us, 64 tokens (~1,058) 115.0 -> 109.5; 3 parts at 64 tokens
 // gain nothing; on the 120B-shaped layer, whose 24 to 64-token batches have 1,610 to
 // 2,770 wide items, 2 parts lose 5 to 9 us.
+// The smallest batches (under 900 gate_up items, 1-2 tokens here) take gate_up items of
+// one gate/up pair over all of K with four chunks in flight instead of the 2 K parts: as
+// many units and bytes per unit, no part sums and no activation launch.  Same box,
+// alternating runs, us per step: 1 token 37.9 -> 36.1 (20B-shaped) and 39.9 -> 37.4
+// (120B-shaped), 2 tokens 50.2 -> 49.9 and 53.3 -> 53.0; 3 tokens (~1,000 items) equal,
+// 4 tokens (~1,300) 0.9-1.3 us slower.
+constexpr double kTkgGateUpPairItems = 900.0;
 constexpr double kTkgGateUpSplitItems = 2000.0;
 constexpr double kTkgDownSplitTarget = 1500.0;
 constexpr int kTkgDownMaxParts = 3;
@@ -720,6 +734,7 @@ struct TkgSplit {
   int nq_gu = 1, nq_dn = 1;    // K parts
   int cpq_gu = 1 << 20, cpq_dn = 1 << 20;  // 128-wide chunks per part
   bool one_tile = true;
+  bool gu_pairs = false;       // gate_up items of one gate/up pair, all of K
   bool dn_wide = false;        // down items of 8 row groups, one chunk in flight
 };
 
@@ -738,7 +753,9 @@ static TkgSplit tkg_split(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
   const double active = (double)E * (1.0 - pow(1.0 - (double)K / (double)E, (double)T));
   const double tiles = active + ((double)(T * K) - active) / 16.0;  // 16-token tiles
   const double gu_items = tiles * (double)((2 * I / 16 + 3) / 4);
-  if (gu_items < kTkgGateUpSplitItems) tkg_parts((int)((H + 127) / 128), 2, sp.nq_gu, sp.cpq_gu);
+  sp.gu_pairs = gu_items < kTkgGateUpPairItems;
+  if (!sp.gu_pairs && gu_items < kTkgGateUpSplitItems)
+    tkg_parts((int)((H + 127) / 128), 2, sp.nq_gu, sp.cpq_gu);
   const double wide_items = tiles * (double)((H / 16 + 7) / 8);
   sp.dn_wide = wide_items >= 900.0;
   if (sp.dn_wide) {
@@ -869,11 +886,17 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     gu.cpq = sp.cpq_gu;
     gu.part = w.part;
     gu.part_stride = (size_t)S * 2 * (size_t)I;
-    // One 16-token tile per item; with nq_gu > 1 each item's K in nq_gu parts, whose raw
-    // sums the activation kernel adds in order before the bias, clamps and activation.
-    hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>),
-                       dim3(grid(true, 4, 4, n_tile_max).x * sp.nq_gu), dim3(256), kLds3x4, s,
-                       gu);
+    // One 16-token tile per item of 2 gate/up pairs; with nq_gu > 1 each item's K in
+    // nq_gu parts, whose raw sums the activation kernel adds in order before the bias,
+    // clamps and activation.  The smallest batches: items of one pair, four chunks in
+    // flight.
+    if (sp.gu_pairs)
+      hipLaunchKernelGGL((tkg_stream_kernel<2, 1, true, 4, 4>),
+                         dim3(grid(true, 2, 4, n_tile_max).x), dim3(256), kLds3x4, s, gu);
+    else
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>),
+                         dim3(grid(true, 4, 4, n_tile_max).x * sp.nq_gu), dim3(256), kLds3x4,
+                         s, gu);
     if (sp.nq_gu > 1)
       hipLaunchKernelGGL(tkg_act_kernel, dim3((unsigned)((I + 1023) / 1024), (unsigned)S),
                          dim3(256), 0, s, gu, (int)E);
