@@ -719,13 +719,16 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // (~965 items) 110.2 -> 103.5 us, 64 tokens (~1,058) 115.0 -> 109.5; 3 parts at 64 tokens
 // gain nothing; on the 120B-shaped layer, whose 24 to 64-token batches have 1,610 to
 // 2,770 wide items, 2 parts lose 5 to 9 us.
-// The smallest batches (under 900 gate_up items, 1-2 tokens here) take gate_up items of
-// one gate/up pair over all of K with four chunks in flight instead of the 2 K parts: as
-// many units and bytes per unit, no part sums and no activation launch.  Same box,
-// alternating runs, us per step: 1 token 37.9 -> 36.1 (20B-shaped) and 39.9 -> 37.4
-// (120B-shaped), 2 tokens 50.2 -> 49.9 and 53.3 -> 53.0; 3 tokens (~1,000 items) equal,
-// 4 tokens (~1,300) 0.9-1.3 us slower.
-constexpr double kTkgGateUpPairItems = 900.0;
+// The smallest batches (under 1,300 gate_up items: 1-3 tokens here, and 4 on the 20B
+// shape) take gate_up items of one gate/up pair over all of K, four chunks in flight, in
+// one-wave workgroups, instead of the 2 K parts: as many units and bytes per unit, no
+// part sums and no activation launch, and the waves spread over every CU (a 1-token
+// batch's 720 pair items fill only 180 workgroups of four).  Same box, alternating runs,
+// us per step against the 2 K parts: 20B-shaped layer 1 token 38.0 -> 35.0, 2 tokens
+// 50.4 -> 46.8, 3 tokens 54.8 -> 54.3, 4 tokens (~1,210 items) 60.0 -> 59.2; 120B-shaped
+// 1 token 40.1 -> 36.7, 2 tokens 53.3 -> 50.0, 3 tokens 59.7 -> 58.3.  Pair items at 4
+// tokens on the 120B shape (~1,380 items) measured 67.0 -> 69.0: hence the threshold.
+constexpr double kTkgGateUpPairItems = 1300.0;
 constexpr double kTkgGateUpSplitItems = 2000.0;
 constexpr double kTkgDownSplitTarget = 1500.0;
 constexpr int kTkgDownMaxParts = 3;
@@ -889,10 +892,10 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     // One 16-token tile per item of 2 gate/up pairs; with nq_gu > 1 each item's K in
     // nq_gu parts, whose raw sums the activation kernel adds in order before the bias,
     // clamps and activation.  The smallest batches: items of one pair, four chunks in
-    // flight.
+    // flight, one-wave workgroups.
     if (sp.gu_pairs)
-      hipLaunchKernelGGL((tkg_stream_kernel<2, 1, true, 4, 4>),
-                         dim3(grid(true, 2, 4, n_tile_max).x), dim3(256), kLds3x4, s, gu);
+      hipLaunchKernelGGL((tkg_stream_kernel<2, 1, true, 4, 1>),
+                         dim3(grid(true, 2, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
     else
       hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>),
                          dim3(grid(true, 4, 4, n_tile_max).x * sp.nq_gu), dim3(256), kLds3x4,
