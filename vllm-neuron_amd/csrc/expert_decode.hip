@@ -893,9 +893,16 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     // nq_gu parts, whose raw sums the activation kernel adds in order before the bias,
     // clamps and activation.  The smallest batches: items of one pair, four chunks in
     // flight, one-wave workgroups.
+    // Unsplit batches of up to 16 tokens: one-wave workgroups too (same box, alternating
+    // runs, us per step: 120B-shaped layer 8 / 12 / 16 tokens -1.9 / -1.1 / -1.8, 20B-shaped
+    // 12 / 16 tokens -4.6 / -2.8; at 24-64 tokens on the 20B shape +0.4 to +2.5, at 48
+    // and 64 tokens on the 120B shape +1.6 and +1.0, at 4 split tokens +0.7).
     if (sp.gu_pairs)
       hipLaunchKernelGGL((tkg_stream_kernel<2, 1, true, 4, 1>),
                          dim3(grid(true, 2, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
+    else if (sp.nq_gu == 1 && T <= 16)
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 1>),
+                         dim3(grid(true, 4, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
     else
       hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 4>),
                          dim3(grid(true, 4, 4, n_tile_max).x * sp.nq_gu), dim3(256), kLds3x4,
@@ -919,8 +926,12 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
                          dim3(grid(false, 8, 1, n_tile_max).x * sp.nq_dn), dim3(64), kLds12x1, s,
                          dn);
     } else {
-      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 4>),
-                         dim3(grid(false, 4, 4, n_tile_max).x * sp.nq_dn), dim3(256), kLds3x4, s,
+      // one-wave workgroups (us per step against four-wave ones, same box: 20B-shaped
+      // layer 12 / 16 / 24 / 32 tokens -3.4 / -2.6 / -6.2 / -6.8, 120B-shaped 4 / 8 tokens
+      // -1.5 / -1.4, elsewhere within +-0.7 except 8 tokens on the 20B shape: +1.1, -0.7
+      // and +1.9 in three comparisons)
+      hipLaunchKernelGGL((tkg_stream_kernel<4, 1, false, 2, 1>),
+                         dim3(grid(false, 4, 1, n_tile_max).x * sp.nq_dn), dim3(64), kLds12x1, s,
                          dn);
     }
   } else {
