@@ -174,6 +174,53 @@ def test_derived_cache_never_aliases_freed_storage():
     assert _cache.transposed_rows(v.t()).data_ptr() == v.data_ptr()  # [E, H] storage: a view
 
 
+def test_derived_cache_releases_freed_sources():
+    """An entry never keeps its sources alive: freeing the key frees the entry and its
+    converted copy, a freed second input makes the entry stale, and a value that is a
+    view of the key is returned uncached (it would pin the key)."""
+    import gc
+    import weakref
+
+    import torch
+
+    from vllm_neuron_amd.functional.moe import _cache
+
+    _cache.clear()
+    src = torch.randn(64, 32)
+    other = torch.randn(32)
+    val = _cache.derived("conv", (src, other), lambda: src.t().contiguous() + other[:1])
+    assert _cache.derived("conv", (src, other), lambda: 1 / 0) is val  # a hit
+    assert _cache.entries() == 1
+    w_src, w_val = weakref.ref(src), weakref.ref(val)
+    del src, val
+    gc.collect()
+    assert w_src() is None and w_val() is None  # source and converted copy released
+    assert _cache.entries() == 0
+
+    key = torch.randn(16, 8)
+    b = torch.randn(8)
+    r1 = _cache.derived("sum", (key, b), lambda: key + b)
+    w_b = weakref.ref(b)
+    del b
+    gc.collect()
+    assert w_b() is None  # the entry does not hold its second input
+    b2 = torch.randn(8)
+    r2 = _cache.derived("sum", (key, b2), lambda: key + b2)
+    assert r2 is not r1 and torch.equal(r2, key + b2)
+
+    k2 = torch.randn(4, 4)
+    v1 = _cache.derived("view", (k2,), lambda: k2.view(16))
+    v2 = _cache.derived("view", (k2,), lambda: k2.view(16))
+    assert v1 is not v2  # a view of the key is not cached
+    w_k2 = weakref.ref(k2)
+    del k2, v1, v2
+    gc.collect()
+    assert w_k2() is None
+    del key, b2, r1, r2
+    gc.collect()
+    assert _cache.entries() == 0
+
+
 def test_moe_cte_no_scale_raises():
     import torch
 

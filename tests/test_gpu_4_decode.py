@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from moe_helpers import build, check_close, check_indices, decode_checked
+from moe_helpers import BF16_OUT, build, check_close, check_indices, decode_checked
 
 pytestmark = pytest.mark.gpu
 
@@ -23,7 +23,7 @@ def test_decode_gptoss20b(dev, gptoss20, T):
     x = synthetic.tokens(21, T, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
-    check_close(got, want, ties, f"decode 20b T={T}")
+    check_close(got, want, ties, f"decode 20b T={T}", ulp=BF16_OUT)
 
 
 @pytest.mark.parametrize("E,T,zipf", [(32, 64, 1.2), (64, 48, 1.5)])
@@ -40,7 +40,7 @@ def test_decode_skewed_routing_hot_experts(dev, E, T, zipf):
           f"{int((per_expert > 0).sum())}")
     assert per_expert.max() > 32  # at least three tiles for one expert
     want = ref.decode_routed(x, aff)
-    check_close(got, want, ties, f"decode skewed E={E} T={T} zipf={zipf}")
+    check_close(got, want, ties, f"decode skewed E={E} T={T} zipf={zipf}", ulp=BF16_OUT)
 
 
 @pytest.mark.parametrize("T", [16, 64])
@@ -84,7 +84,7 @@ def test_decode_wide_expert_counts(dev, E, k, T):
     x = synthetic.tokens(41, T, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
-    check_close(got, want, ties, f"decode E={E} k={k} T={T}")
+    check_close(got, want, ties, f"decode E={E} k={k} T={T}", ulp=BF16_OUT)
 
 
 @pytest.mark.parametrize("T", [200, 256])
@@ -96,9 +96,8 @@ def test_decode_large_batch(dev, gptoss20, T):
     ref, layer, _ = gptoss20
     x = synthetic.tokens(33, T, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
-    rows = torch.arange(0, T, 7)
-    want = ref.decode_routed(x[rows], aff[rows])
-    check_close(got[rows], want, ties[rows], f"decode 20b T={T} sample")
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, f"decode 20b T={T}", ulp=BF16_OUT)
 
 
 def test_decode_unsaturated_weights(dev):
@@ -108,7 +107,7 @@ def test_decode_unsaturated_weights(dev):
     x = synthetic.tokens(22, 40, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
-    check_close(got, want, ties, "decode unsaturated")
+    check_close(got, want, ties, "decode unsaturated", ulp=BF16_OUT)
 
 
 def test_decode_dense_flow_equals_routed(dev):
@@ -130,7 +129,7 @@ def test_decode_plain_swiglu_fine_grained(dev):
     x = synthetic.tokens(24, 8, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
-    check_close(got, want, ties, "decode plain swiglu")
+    check_close(got, want, ties, "decode plain swiglu", ulp=BF16_OUT)
 
 
 def test_moe_tkg_api_ep_rank_and_no_scale(dev):
@@ -255,14 +254,12 @@ def test_moe_block_tkg_api_expert_slice(dev):
     check_close(out.cpu(), want, None, "moe_block_tkg expert slice")
 
 
-def test_decode_gptoss120b_t64_sample(dev):
-    """120B-shaped layer (128 experts) at 64 tokens: a sample of 8 tokens against the
-    oracle (per-token outputs depend only on the token's own row and routing)."""
+def test_decode_gptoss120b_t64(dev):
+    """120B-shaped layer (128 experts) at 64 tokens, every token against the oracle."""
     from vllm_neuron_amd import synthetic
 
     ref, layer, _ = build(synthetic.GPT_OSS_120B, 7, dev)
     x = synthetic.tokens(27, 64, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
-    rows = torch.arange(0, 64, 8)
-    want = ref.decode_routed(x[rows], aff[rows])
-    check_close(got[rows], want, ties[rows], "decode 120b T=64 sample")
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, "decode 120b T=64", ulp=BF16_OUT)

@@ -1,20 +1,23 @@
-"""The two largest workload shapes against the oracle, on sampled tokens.
+"""The two largest workload shapes against the oracle.
 
 * GPT-OSS-120B-shaped layer (E=128, top-4, H=I=2880) at prefill, 4096 tokens, uniform
   routing and Zipf(1.2)-skewed routing: 382 M-tiles of 128 slots, the shape the
-  prefill GEMMs are tuned for.
+  prefill GEMMs are tuned for.  Every token row is checked, with fp32 output (the
+  reference flow's own result type) against a regression bound at the achieved level,
+  and with bf16 output (the layer's default) against the tolerance.
 * Fine-grained layer (E=256, top-8, H=7168, I=2048, plain SwiGLU, no biases) with
-  Zipf(1.0) routing, decode at 128 tokens and prefill at 8192 tokens.
-Per-token outputs depend only on the token's own row and routing, so a sample of rows
-checked against the oracle's routed forms (weights dequantized per expert on first
-use) tests the whole batch's schedule.  Routing indices are compared exactly for every
-token (near-ties exempted and counted).
+  Zipf(1.0) routing: decode at 128 tokens on every row; prefill at 8192 tokens on the
+  rows that reach every M-tile of every expert (first and last token of each expert and
+  both sides of every 128-slot tile boundary) plus random rows.
+The oracle's routed forms dequantize each expert on first use.  Routing indices are
+compared exactly for every token (near-ties exempted and counted).
 """
 
 import pytest
 import torch
 
-from moe_helpers import build, check_close, decode_checked, routing_agreement
+from moe_helpers import (BF16_OUT, PREFILL_FP32_MEAN, PREFILL_FP32_MEAN_PLAIN, build,
+                         check_close, decode_checked, routing_agreement, stratified_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -44,14 +47,18 @@ def test_prefill_gptoss120b_t4096(dev, zipf):
     T = 4096
     x = synthetic.tokens(84, T, ref.H)
     aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.prefill(x.to(dev)).cpu()
+    xd = x.to(dev)
+    got32 = layer.prefill(xd, output_dtype=torch.float32).cpu()
+    got16 = layer.prefill(xd).cpu()
     torch.cuda.synchronize()
-    rows = torch.arange(3, T, T // 40)
-    _say(f"oracle on {len(rows)} rows")
-    want = ref.prefill_routed(x, aff, token_rows=rows)
+    _say("oracle on all rows")
+    want = ref.prefill_routed(x, aff)
     per_expert = (aff != 0).sum(0)
     _say(f"tokens per expert: max {int(per_expert.max())}, min {int(per_expert.min())}")
-    check_close(got[rows], want, ties[rows], f"prefill 120b T=4096 zipf={zipf}")
+    check_close(got32, want, ties, f"prefill 120b T=4096 zipf={zipf} fp32",
+                mean_bound=PREFILL_FP32_MEAN)
+    check_close(got16, want.to(torch.bfloat16), ties, f"prefill 120b T=4096 zipf={zipf} bf16",
+                ulp=BF16_OUT)
 
 
 @pytest.mark.timeout(600)
@@ -62,10 +69,8 @@ def test_decode_fine_grained_t128(dev, fine_grained):
     T = 128
     x = synthetic.tokens(85, T, ref.H)
     got, aff, ties = decode_checked(layer, ref, x, dev)
-    rows = torch.arange(0, T, 8)
-    _say(f"oracle on {len(rows)} rows")
-    want = ref.decode_routed(x[rows], aff[rows])
-    check_close(got[rows], want, ties[rows], "decode 256x8 T=128 zipf=1.0")
+    want = ref.decode_routed(x, aff)
+    check_close(got, want, ties, "decode 256x8 T=128 zipf=1.0", ulp=BF16_OUT)
 
 
 @pytest.mark.timeout(600)
@@ -76,9 +81,10 @@ def test_prefill_fine_grained_t8192(dev, fine_grained):
     T = 8192
     x = synthetic.tokens(86, T, ref.H)
     aff, ties = routing_agreement(layer, ref, x, dev)
-    got = layer.prefill(x.to(dev)).cpu()
+    got = layer.prefill(x.to(dev), output_dtype=torch.float32).cpu()
     torch.cuda.synchronize()
-    rows = torch.arange(5, T, T // 24)
-    _say(f"oracle on {len(rows)} rows")
+    rows = stratified_rows(aff, extra=256, seed=86)
+    _say(f"oracle on {len(rows)} rows (every M-tile of every expert)")
     want = ref.prefill_routed(x, aff, token_rows=rows)
-    check_close(got[rows], want, ties[rows], "prefill 256x8 T=8192 zipf=1.0")
+    check_close(got[rows], want, ties[rows], "prefill 256x8 T=8192 zipf=1.0 fp32",
+                mean_bound=PREFILL_FP32_MEAN_PLAIN)

@@ -1,17 +1,23 @@
 """Tensors derived once from a caller's parameters (transposed router weights, weights
 converted from another layout), cached per source tensor and version.
 
-An entry lives as long as the source's base tensor (a weak identity-keyed map), so
-freed storage whose address is reused by a new tensor can never hit an old entry.
-Each entry records the signature of every input it was made from (base identity,
-view geometry, dtype, version counter) and holds those bases, so the identities it
-compares stay valid while it exists; an in-place update bumps the version and makes
-the entry stale.  Inference tensors have no version counter: they are never cached, and
-nothing made while a HIP graph is being captured on the current stream is kept.
+An entry lives only as long as the source's base tensor: the map is keyed weakly by that
+base, and the entry refers to its other inputs' bases through weak references too, so a
+cached value never keeps any of the tensors it was made from alive.  When the key's base
+is freed, the entry and the value go with it.  Each entry records the signature of every
+input it was made from (base identity, view geometry, dtype, version counter) together
+with a weak reference to each base; a hit requires every reference to be alive and to
+name the very base the caller passes, so freed storage whose address (or ``id``) is
+reused by a new tensor can never hit an old entry, and an in-place update (a version
+bump) makes the entry stale.  A value that is itself a view of the key's base would keep
+the key alive, and is therefore returned without being cached.  Inference tensors have
+no version counter: they are never cached, and nothing made while a HIP graph is being
+captured on the current stream is kept.
 """
 
 from __future__ import annotations
 
+import weakref
 from typing import Callable, Optional, Sequence
 
 import torch
@@ -40,6 +46,25 @@ def _capturing(inputs: Sequence[Optional[Tensor]]) -> bool:
     return t is not None and t.is_cuda and torch.cuda.is_current_stream_capturing()
 
 
+def _tensors(value):
+    """The tensors a cached value holds (a tensor, or a tuple / named tuple of them)."""
+    if isinstance(value, Tensor):
+        return [value]
+    if isinstance(value, (tuple, list)):
+        return [t for v in value for t in _tensors(v)]
+    return []
+
+
+def _refs_alive(refs, inputs) -> bool:
+    """Every input's base is still the object the entry was made from."""
+    for r, t in zip(refs, inputs):
+        if (r is None) != (t is None):
+            return False
+        if r is not None and r() is not _base(t):
+            return False
+    return True
+
+
 def derived(tag: str, inputs: Sequence[Optional[Tensor]], make: Callable[[], object]):
     """``make()`` computed from ``inputs`` (the first one is the key), cached until any
     input is freed, replaced by another tensor or modified in place."""
@@ -47,20 +72,29 @@ def derived(tag: str, inputs: Sequence[Optional[Tensor]], make: Callable[[], obj
     if any(t is not None and t.is_inference() for t in inputs):
         with torch.no_grad():
             return make()
+    kb = _base(key)
     sig = (tag,) + tuple(_signature(t) for t in inputs)
-    slot = _ENTRIES.get(_base(key))
+    slot = _ENTRIES.get(kb)
     hit = None if slot is None else slot.get(tag)
-    if hit is not None and hit[0] == sig:
+    if hit is not None and hit[0] == sig and _refs_alive(hit[1], inputs):
         return hit[2]
     with torch.no_grad():
         value = make()
     if _capturing(inputs):  # the value lives in the graph's pool: used, not kept
         return value
+    if any(_base(t) is kb for t in _tensors(value)):  # a view of the key would pin it
+        return value
     if slot is None:
         slot = {}
-        _ENTRIES[_base(key)] = slot
-    slot[tag] = (sig, [None if t is None else _base(t) for t in inputs], value)
+        _ENTRIES[kb] = slot
+    refs = [None if t is None else weakref.ref(_base(t)) for t in inputs]
+    slot[tag] = (sig, refs, value)
     return value
+
+
+def entries() -> int:
+    """Number of live source tensors with cached values."""
+    return len(_ENTRIES)
 
 
 def clear() -> None:
