@@ -23,15 +23,24 @@ covers the prefill gate_up GEMM (MFMA bound, bf16 MFMA after in-register dequant
 Before the per-kernel timing pass and again right before each timed region the step runs
 untimed for ``--settle`` seconds (0.3 by default; counts reported as ``settle_steps``): a
 GPU that has been idle reaches its steady clocks only after a few hundred milliseconds of
-work, and a short timed region otherwise measures the clock ramp.  The timed region is
-exactly the requested steps.
+work, and a short timed region otherwise measures the clock ramp.  The decode steps are
+replayed from a HIP graph of up to 40 consecutive steps, so the timed count is the requested
+steps rounded down to a multiple of the graph's length (``steps`` in the JSON is the count
+timed); prefill times exactly ``--prefill-steps`` eager steps.
+
+``other_configs`` (default workload only) times the benchmark's other workloads once each,
+with their binding-roofline fractions: the MXFP4 linear (W 5760 x 2880, x 128 x 2880), the
+GPT-OSS-20B-shaped layer at decode (1, 4, 16 and 64 tokens) and prefill (4,096 tokens,
+uniform and Zipf(1.2) routing), and the 256-expert top-8 layer (H 7168, I 2048, Zipf(1.0)
+routing) at decode (128 tokens) and prefill (8,192 tokens).
 
 ``--weights bf16`` times the bf16-expert path instead (the reference's shard_on_block
 operands; moe_cte prefill and moe_block_tkg decode) and prints a line of its own.
 
 ``cpu_baseline`` times the CPU oracle (a port of the reference's CPU flow: dense
-all-expert fp32 decode, dense all-expert bf16 prefill) on the host cores over a
-bounded sample of experts / tokens and scales linearly to the full workload.
+all-expert fp32 decode, dense all-expert bf16 prefill) on every affinity core of the host,
+over the full expert set: decode on the whole batch, prefill on a 256-token slice (linear in
+tokens).
 """
 
 from __future__ import annotations
@@ -73,6 +82,9 @@ def parse():
     ap.add_argument("--zipf", type=float, default=None,
                     help="routing skew: router bias -s*log(1 + rank) over a random expert order")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the other workloads (MXFP4 linear, 20B-shaped decode and prefill, "
+                         "256-expert decode and prefill) reported in other_configs")
     ap.add_argument("--no-graph", action="store_true", help="time decode with eager launches")
     ap.add_argument("--settle", type=float, default=0.3,
                     help="seconds of untimed steps after the warmup and again right before "
@@ -156,8 +168,34 @@ def measured_traffic(workload, decode_T, prefill_T):
     return dec, pre, d["source"]
 
 
-def cpu_baseline(wl, decode_T, prefill_T):
-    """Time the CPU oracle on a bounded sample; returns dicts for decode and prefill."""
+def cpu_model() -> str:
+    """The host CPU's model name as lscpu reports it (/proc/cpuinfo if lscpu fails)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for ln in out.splitlines():
+            if ln.strip().lower().startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                        "unknown")
+    except OSError:
+        return "unknown"
+
+
+def cpu_baseline(wl, decode_T, prefill_T, prefill_slice=256):
+    """Time the CPU oracle (the reference's CPU flows) on every affinity core of this host,
+    over the workload's full expert set.  Decode: the dense all-expert fp32 flow of
+    moe_block_tkg on the whole batch (its cost is the per-call fp32 cast and product of
+    every expert's weights, not linear in tokens).  Prefill: the dense all-expert bf16
+    _torch_moe_impl flow on a slice of the tokens, scaled linearly to the batch (every
+    product in it is linear in the token count).  Weights are bf16 values of the layer's
+    shapes (one random expert repeated: the arithmetic and its cost do not depend on the
+    values).  Returns dicts for decode and prefill."""
     import torch
 
     import pkgload
@@ -168,50 +206,47 @@ def cpu_baseline(wl, decode_T, prefill_T):
     from oracle.layer import RefLayer
 
     E, K, H, I, limit, biases, _, _ = WORKLOADS[wl]
-    # The process's affinity cores, at most 16: the host share one GPU's jobs get on a
-    # node of 8 GPUs, whatever the affinity mask shows.
-    affinity = len(os.sched_getaffinity(0))
-    cores = min(affinity, 16)
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
-                         "unknown")
-    except OSError:
-        pass
-    e_s = min(E, 16)
-    shape = synthetic.MoEShape(wl + "-sample", E, min(K, e_s), H, I, limit, biases)
-    ref = RefLayer(synthetic.layer_tensors(shape, 5, E=e_s))
+    model = cpu_model()
+    g = torch.Generator().manual_seed(5)
 
-    def timed(fn, budget_s):
+    def rn(*shape, std):
+        return (torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+
+    gu = rn(1, H, 2 * I, std=H ** -0.5).repeat(E, 1, 1)
+    dn = rn(1, I, H, std=I ** -0.5).repeat(E, 1, 1)
+    gub = rn(E, 2 * I, std=0.02) if biases else None
+    dnb = rn(E, H, std=0.02) if biases else None
+    ref = RefLayer.from_dense(gu, dn, gub, dnb, rn(E, H, std=0.02), None, K, limit)
+
+    def timed(fn, reps):
         fn()  # warm-up
         ts = []
-        while len(ts) < 3 or sum(ts) < budget_s:
+        for _ in range(reps):
             t0 = time.perf_counter()
             fn()
             ts.append(time.perf_counter() - t0)
         return sorted(ts)[len(ts) // 2], len(ts)
 
+    base = {"unit": "tokens/s", "cores": cores, "kind": "port", "cpu": model,
+            "affinity_cores": cores}
     res = {}
     x = synthetic.tokens(5, decode_T, H)
-    t, n = timed(lambda: ref.decode(x), 8.0)
-    t *= E / e_s
-    res["decode"] = {"value": decode_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
-                     "cpu": model, "affinity_cores": affinity,
-                     "sample": f"dense all-expert fp32 decode (reference moe_block_tkg CPU flow) "
-                               f"of {decode_T} tokens over {e_s} of {E} experts, median of {n} "
-                               f"reps (about 8 s), time scaled x{E / e_s:g} (linear in experts)"}
-    t_s = min(prefill_T, 512)
+    t, n = timed(lambda: ref.decode(x), 3)
+    res["decode"] = dict(base, value=decode_T / t,
+                         sample=f"dense all-expert fp32 decode (reference moe_block_tkg CPU flow) "
+                                f"of all {decode_T} tokens over all {E} experts, median of {n} "
+                                f"reps after one warm-up, {t:.2f} s per call, unscaled")
+    t_s = min(prefill_T, prefill_slice)
     xp = synthetic.tokens(6, t_s, H)
-    t, n = timed(lambda: ref.prefill(xp), 8.0)
-    t *= (E / e_s) * (prefill_T / t_s)
-    res["prefill"] = {"value": prefill_T / t, "unit": "tokens/s", "cores": cores, "kind": "port",
-                      "cpu": model, "affinity_cores": affinity,
-                      "sample": f"dense all-expert bf16 prefill (reference _torch_moe_impl CPU "
-                                f"flow) of {t_s} tokens over {e_s} of {E} experts, median of {n} "
-                                f"reps (about 8 s), time scaled x{E / e_s:g} (experts) "
-                                f"x{prefill_T / t_s:g} (tokens)"}
+    t, n = timed(lambda: ref.prefill(xp), 3)
+    res["prefill"] = dict(base, value=t_s / t,
+                          sample=f"dense all-expert bf16 prefill (reference _torch_moe_impl CPU "
+                                 f"flow) of a {t_s}-token slice over all {E} experts, median of "
+                                 f"{n} reps after one warm-up, {t:.2f} s per call; tokens/s of "
+                                 f"the slice (the flow is linear in tokens, so the "
+                                 f"{prefill_T}-token batch takes x{prefill_T / t_s:g} the time)")
     return res
 
 
@@ -310,6 +345,271 @@ def bench_bf16(args):
     print(json.dumps(out))
 
 
+def _ev():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True)
+
+
+def settle(step_fn, seconds):
+    """Untimed steps for ``seconds`` of wall time (the GPU leaves its idle clocks within a
+    few hundred milliseconds of sustained work); returns the steps run."""
+    import torch
+
+    n, end = 0, time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(8):
+            n += step_fn(n)
+        torch.cuda.synchronize()
+    return n
+
+
+def time_decode(layers, xs, touched, wl_shape, steps, warmup, settle_s, graph=True,
+                kernel_steps=100):
+    """Decode steps over the rotated layers: per-kernel durations from an eager pass with
+    the library's stage events, then ``steps`` timed steps replayed from a HIP graph of up
+    to 40 consecutive steps (``steps`` rounded down to a multiple of the graph's length;
+    the JSON reports the count timed).  Returns the decode dict."""
+    import torch
+
+    E, K, H, I, limit, biases = wl_shape
+    L = len(layers)
+    dT = xs[0].shape[0]
+    for s in range(warmup):
+        layers[s % L].decode(xs[s % L])
+    torch.cuda.synchronize()
+
+    def eager_step(n):
+        layers[n % L].decode(xs[n % L])
+        return 1
+
+    settled = settle(eager_step, settle_s)
+    # Per-kernel durations: an eager pass with the library's stage events on the launch
+    # stream (events recorded inside a captured graph do not time its kernels).
+    n_ev = kernel_steps
+    stage = [[_ev() for _ in range(6)] for _ in range(n_ev)]
+    e0, e1 = _ev(), _ev()
+    e0.record()
+    for s in range(n_ev):
+        layers[s % L].decode(xs[s % L], stage_events=stage[s])
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / n_ev
+
+    mode = "eager"
+    if graph:
+        # One graph holds G consecutive steps over the rotated layers (a layer recurs at
+        # least 4 steps later, across replays).
+        G = min(steps, 40)
+        reps = max(1, steps // G)
+        steps = G * reps
+        try:
+            g = torch.cuda.CUDAGraph()
+            cap_stream = torch.cuda.Stream()
+            cap_stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(cap_stream):
+                with torch.cuda.graph(g, stream=cap_stream):
+                    for s in range(G):
+                        layers[s % L].decode(xs[s % L])
+            torch.cuda.current_stream().wait_stream(cap_stream)
+            g.replay()
+            torch.cuda.synchronize()
+            mode = "hip-graph"
+        except Exception as exc:  # capture unsupported: time eagerly
+            print(f"graph capture failed ({exc}); timing eagerly", file=sys.stderr)
+            torch.cuda.synchronize()
+    if mode == "hip-graph":
+        settled += settle(lambda n: (g.replay(), G)[1], settle_s)
+    else:
+        settled += settle(eager_step, settle_s)
+    t0, t1 = _ev(), _ev()
+    t0.record()
+    if mode == "hip-graph":
+        for _ in range(reps):
+            g.replay()
+    else:
+        for s in range(steps):
+            layers[s % L].decode(xs[s % L])
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+
+    def stage_ms(a, b):
+        return sum(stage[s][a].elapsed_time(stage[s][b]) for s in range(n_ev)) / n_ev
+
+    avg_touched = sum(touched[s % L] for s in range(steps)) / steps
+    layer_bytes = avg_touched * bytes_per_expert(H, I, biases) + E * H * 2 + 2 * dT * H * 2
+    ev_touched = sum(touched[s % L] for s in range(n_ev)) / n_ev
+    gu_bytes = ev_touched * gate_up_bytes_per_expert(H, I, biases) + dT * H * 2
+    return {
+        "tokens_per_s": dT / (ms * 1e-3), "ms_per_step": ms, "steps": steps,
+        "experts_touched_avg": avg_touched,
+        "layer_algorithmic_bytes": layer_bytes,
+        "layer_GBps": layer_bytes / (ms * 1e-3) / 1e9,
+        "layer_frac_hbm": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_ms": {"router": stage_ms(0, 1), "route": stage_ms(1, 2),
+                      "gate_up": stage_ms(2, 3), "down": stage_ms(3, 4),
+                      "combine": stage_ms(4, 5)},
+        "gate_up_algorithmic_bytes": gu_bytes,
+        "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
+        "settle_steps": settled, "settle_s": 2 * settle_s,
+    }
+
+
+def time_prefill(layers, xps, wl_shape, steps, settle_s, warmup=3):
+    """Prefill steps over the rotated layers (eager launches): per-kernel durations from a
+    pass with the library's stage events, then ``steps`` timed steps that record none.
+    Returns the prefill dict."""
+    import torch
+
+    E, K, H, I, limit, biases = wl_shape
+    L = len(layers)
+    pT = xps[0].shape[0]
+    for s in range(warmup):
+        layers[s % L].prefill(xps[s % L])
+    torch.cuda.synchronize()
+    p_settled = settle(lambda n: (layers[n % L].prefill(xps[n % L]), 1)[1], settle_s)
+    # Each event recorded between two kernels of the step delays the next one by a few
+    # microseconds, so the timed region below records none.
+    pst = [[_ev() for _ in range(4)] for _ in range(steps)]
+    for s in range(steps):
+        layers[s % L].prefill(xps[s % L], stage_events=pst[s])
+    torch.cuda.synchronize()
+    gu_ms = sum(pst[s][0].elapsed_time(pst[s][1]) for s in range(steps)) / steps
+    dn_ms = sum(pst[s][1].elapsed_time(pst[s][2]) for s in range(steps)) / steps
+    cb_ms = sum(pst[s][2].elapsed_time(pst[s][3]) for s in range(steps)) / steps
+    p0, p1 = _ev(), _ev()
+    p0.record()
+    for s in range(steps):
+        layers[s % L].prefill(xps[s % L])
+    p1.record()
+    torch.cuda.synchronize()
+    pms = p0.elapsed_time(p1) / steps
+    pairs = pT * K
+    flops = 6 * H * I * pairs + 2 * pT * H * E
+    gu_flops = 4 * H * I * pairs
+    pbytes = E * bytes_per_expert(H, I, biases) + E * H * 2 + 2 * pT * H * 2
+    gu_tf = gu_flops / (gu_ms * 1e-3) / 1e12
+    t_min = max(pbytes / (HBM_PEAK_GBS * 1e9), flops / (MXFP4_PEAK_TFLOPS * 1e12))
+    return {
+        "value": pT / (pms * 1e-3), "unit": "tokens/s", "ms_per_step": pms, "tokens": pT,
+        "steps": steps, "settle_steps": p_settled, "algorithmic_flops": flops,
+        "algorithmic_bytes": pbytes,
+        "layer_TFLOPs": flops / (pms * 1e-3) / 1e12,
+        "layer_frac_mxfp4_peak": flops / (pms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS,
+        "layer_frac_bf16_peak": flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "layer_frac_binding_roofline": t_min / (pms * 1e-3),
+        "binding_roofline": "hbm" if pbytes / (HBM_PEAK_GBS * 1e9) >= flops / (
+            MXFP4_PEAK_TFLOPS * 1e12) else "mxfp4 mfma",
+        "kernel_ms": {"gate_up": gu_ms, "down": dn_ms, "combine": cb_ms,
+                      "router+mapping": pms - gu_ms - dn_ms - cb_ms},
+        "gate_up_TFLOPs": gu_tf, "gate_up_frac_bf16_peak": gu_tf / BF16_PEAK_TFLOPS,
+        "gate_up_algorithmic_flops": gu_flops,
+    }
+
+
+def build_workload(wl, n_layers, dev, gen, zipf=None):
+    E, K, H, I, limit, biases, _, _ = WORKLOADS[wl]
+    return [make_layer(E, K, H, I, limit, biases, dev, gen, zipf) for _ in range(n_layers)]
+
+
+def experts_touched(layers, xs):
+    import torch
+
+    out = []
+    for lay, x in zip(layers, xs):
+        _, _, idx, _ = lay.route(x)
+        out.append(int(torch.unique(idx).numel()))
+    torch.cuda.synchronize()
+    return out
+
+
+def time_linear(dev, gen, settle_s, n_w=64, calls=256):
+    """The single MXFP4 weight-only linear: W [5760 x 2880] (codes uniform, exponents
+    uniform in [120, 130]), x bf16 [128 x 2880], fp32 accumulate, bf16 out.  ``n_w``
+    distinct weight matrices are rotated (560 MB, so no call finds its weights in the
+    256 MB last-level cache); the calls are replayed from a HIP graph."""
+    import torch
+
+    from vllm_neuron_amd.functional.mxfp4 import mxfp4_linear
+
+    N, K, M = 5760, 2880, 128
+    ws = [(torch.randint(0, 256, (N // 16, 8 * K), dtype=torch.uint8, device=dev, generator=gen),
+           torch.randint(120, 131, ((N + 63) // 64, 2 * K), dtype=torch.uint8, device=dev,
+                         generator=gen)) for _ in range(n_w)]
+    x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+    for q, sc in ws[:4]:
+        mxfp4_linear(x, q, sc)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(calls):
+                q, sc = ws[i % n_w]
+                mxfp4_linear(x, q, sc)
+    torch.cuda.current_stream().wait_stream(cap)
+    torch.cuda.synchronize()
+    settle(lambda n: (g.replay(), calls)[1], settle_s)
+    t0, t1 = _ev(), _ev()
+    t0.record()
+    for _ in range(4):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / (4 * calls)
+    nbytes = N * K // 2 + N * K // 32 + M * K * 2 + M * N * 2
+    flops = 2 * M * N * K
+    t_min = max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (MXFP4_PEAK_TFLOPS * 1e12))
+    return {"workload": "MXFP4 linear W 5760x2880, x 128x2880 (config 0)", "us_per_call": us,
+            "tokens_per_s": M / (us * 1e-6), "algorithmic_bytes": nbytes,
+            "algorithmic_flops": flops, "GBps": nbytes / (us * 1e-6) / 1e9,
+            "TFLOPs": flops / (us * 1e-6) / 1e12, "binding_roofline": "hbm",
+            "frac_binding_roofline": t_min / (us * 1e-6), "launch": "hip-graph",
+            "calls": 4 * calls}
+
+
+def other_configs(dev, gen, settle_s):
+    """The other workloads of the benchmark, each timed once (hip-graph decode, eager
+    prefill), with its binding-roofline fraction: the MXFP4 linear; the GPT-OSS-20B-shaped
+    layer at decode (1, 4, 16, 64 tokens) and at prefill (4,096 tokens, uniform and
+    Zipf(1.2) routing); the 256-expert top-8 layer with Zipf(1.0) routing at decode (128
+    tokens) and prefill (8,192 tokens).  Each workload rotates over 8 layers."""
+    import torch
+
+    res = {"linear": time_linear(dev, gen, settle_s)}
+    for wl, zipfs, dts in (("gptoss20b", (None, 1.2), (1, 4, 16, 64)), ("fine256", (1.0,), (128,))):
+        E, K, H, I, limit, biases, _, pT = WORKLOADS[wl]
+        shape = (E, K, H, I, limit, biases)
+        for zipf in zipfs:
+            layers = build_workload(wl, 8, dev, gen, zipf)
+            tag = wl + ("" if zipf is None else f"_zipf{zipf:g}")
+            if wl == "fine256" or zipf is None:
+                for dT in dts:
+                    xs = [torch.randn(dT, H, device=dev, generator=gen).to(torch.bfloat16)
+                          for _ in range(8)]
+                    d = time_decode(layers, xs, experts_touched(layers, xs), shape, 40, 3,
+                                    settle_s, kernel_steps=16)
+                    res[f"{tag}_decode_T{dT}"] = {
+                        "tokens_per_s": d["tokens_per_s"], "ms_per_step": d["ms_per_step"],
+                        "experts_touched_avg": d["experts_touched_avg"],
+                        "binding_roofline": "hbm", "frac_binding_roofline": d["layer_frac_hbm"],
+                        "GBps": d["layer_GBps"], "kernel_ms": d["kernel_ms"],
+                        "launch": d["launch"]}
+            xps = [torch.randn(pT, H, device=dev, generator=gen).to(torch.bfloat16)
+                   for _ in range(8)]
+            p = time_prefill(layers, xps, shape, 8, settle_s)
+            res[f"{tag}_prefill_T{pT}"] = {
+                k: p[k] for k in ("value", "ms_per_step", "layer_TFLOPs", "binding_roofline",
+                                  "layer_frac_binding_roofline", "layer_frac_mxfp4_peak",
+                                  "layer_frac_bf16_peak", "gate_up_frac_bf16_peak",
+                                  "kernel_ms")}
+            del layers, xps
+            torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -329,122 +629,24 @@ def main():
 
     dev = torch.device("cuda:0")
     E, K, H, I, limit, biases, dT, pT = WORKLOADS[args.workload]
+    shape = (E, K, H, I, limit, biases)
     dT = args.decode_tokens or dT
     pT = args.prefill_tokens or pT
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     n_layers = args.layers or (36 if args.workload == "gptoss120b" else 8)
-    layers = [make_layer(E, K, H, I, limit, biases, dev, gen, args.zipf) for _ in range(n_layers)]
+    layers = build_workload(args.workload, n_layers, dev, gen, args.zipf)
     L = len(layers)
     xs = [torch.randn(dT, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(L)]
     torch.cuda.synchronize()
+    touched = experts_touched(layers, xs)  # from the actual routing
 
-    # experts touched by each (layer, batch) pair, from the actual routing
-    touched = []
-    for lay, x in zip(layers, xs):
-        _, _, idx, _ = lay.route(x)
-        touched.append(int(torch.unique(idx).numel()))
-    torch.cuda.synchronize()
-
-    def ev():
-        return torch.cuda.Event(enable_timing=True)
-
-    def settle(step_fn, seconds):
-        """Untimed steps for ``seconds`` of wall time (the GPU leaves its idle clocks within
-        a few hundred milliseconds of sustained work); returns the steps run."""
-        n, end = 0, time.perf_counter() + seconds
-        while time.perf_counter() < end:
-            for _ in range(8):
-                n += step_fn(n)
-            torch.cuda.synchronize()
-        return n
-
-    def eager_step(n):
-        layers[n % L].decode(xs[n % L])
-        return 1
-
-    # ---------------- decode
-    for s in range(args.warmup):
-        layers[s % L].decode(xs[s % L])
-    torch.cuda.synchronize()
-    settled = settle(eager_step, args.settle)
-
-    # Per-kernel durations: an eager pass with the library's stage events on the launch
-    # stream (events recorded inside a captured graph do not time its kernels).
-    n_ev = 100
-    stage = [[ev() for _ in range(6)] for _ in range(n_ev)]
-    e0, e1 = ev(), ev()
-    e0.record()
-    for s in range(n_ev):
-        layers[s % L].decode(xs[s % L], stage_events=stage[s])
-    e1.record()
-    torch.cuda.synchronize()
-    eager_ms = e0.elapsed_time(e1) / n_ev
-
-    steps = args.steps
-    mode = "eager"
-    if not args.no_graph:
-        # One graph holds G consecutive steps over the rotated layers (a layer recurs at
-        # least 4 steps later, across replays); the timed region replays it, so ``steps``
-        # is rounded to a multiple of G.
-        G = min(steps, 40)
-        reps = max(1, steps // G)
-        steps = G * reps
-        try:
-            graph = torch.cuda.CUDAGraph()
-            cap_stream = torch.cuda.Stream()
-            cap_stream.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(cap_stream):
-                with torch.cuda.graph(graph, stream=cap_stream):
-                    for s in range(G):
-                        layers[s % L].decode(xs[s % L])
-            torch.cuda.current_stream().wait_stream(cap_stream)
-            graph.replay()
-            torch.cuda.synchronize()
-            mode = "hip-graph"
-        except Exception as exc:  # capture unsupported: time eagerly
-            print(f"graph capture failed ({exc}); timing eagerly", file=sys.stderr)
-            torch.cuda.synchronize()
-    if mode == "hip-graph":
-        settled += settle(lambda n: (graph.replay(), G)[1], args.settle)
-    else:
-        settled += settle(eager_step, args.settle)
-    t0, t1 = ev(), ev()
-    if mode == "hip-graph":
-        t0.record()
-        for _ in range(reps):
-            graph.replay()
-        t1.record()
-    else:
-        t0.record()
-        for s in range(steps):
-            layers[s % L].decode(xs[s % L])
-        t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
-
-    def stage_ms(a, b):
-        return sum(stage[s][a].elapsed_time(stage[s][b]) for s in range(n_ev)) / n_ev
-
-    rt_ms, route_ms, gu_ms = stage_ms(0, 1), stage_ms(1, 2), stage_ms(2, 3)
-    dn_ms, cb_ms = stage_ms(3, 4), stage_ms(4, 5)
-    avg_touched = sum(touched[s % L] for s in range(steps)) / steps
-    bpe = bytes_per_expert(H, I, biases)
-    layer_bytes = avg_touched * bpe + E * H * 2 + 2 * dT * H * 2
-    # the roofline kernel's duration comes from the eager pass over n_ev steps
-    ev_touched = sum(touched[s % L] for s in range(n_ev)) / n_ev
-    gu_bytes = ev_touched * gate_up_bytes_per_expert(H, I, biases) + dT * H * 2
-    decode = {
-        "tokens_per_s": dT / (ms * 1e-3), "ms_per_step": ms,
-        "experts_touched_avg": avg_touched,
-        "layer_algorithmic_bytes": layer_bytes,
-        "layer_GBps": layer_bytes / (ms * 1e-3) / 1e9,
-        "layer_frac_hbm": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "kernel_ms": {"router": rt_ms, "route": route_ms, "gate_up": gu_ms, "down": dn_ms,
-                      "combine": cb_ms},
-        "launch": mode, "eager_ms_per_step": eager_ms, "kernel_timing_steps": n_ev,
-        "settle_steps": settled, "settle_s": 2 * args.settle,
-    }
+    # ---------------- decode (the headline)
+    decode = time_decode(layers, xs, touched, shape, args.steps, args.warmup, args.settle,
+                         graph=not args.no_graph)
+    steps, ms = decode["steps"], decode["ms_per_step"]
+    gu_ms = decode["kernel_ms"]["gate_up"]
+    gu_bytes = decode.pop("gate_up_algorithmic_bytes")
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
     traffic, traffic_pre, traffic_src = measured_traffic(args.workload, dT, pT)
     roofline = {"bound": "hbm", "kernel": "tkg_stream_kernel<4, 1, true, 2, 4> (gate_up)",
@@ -456,50 +658,23 @@ def main():
     prefill = None
     if not args.skip_prefill:
         xp = [torch.randn(pT, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(L)]
-        for s in range(3):
-            layers[s % L].prefill(xp[s % L])
-        torch.cuda.synchronize()
-        p_settled = settle(lambda n: (layers[n % L].prefill(xp[n % L]), 1)[1], args.settle)
-        ps = args.prefill_steps
-        # Per-kernel durations from a pass with the library's stage events; the timed
-        # region below records none (each event recorded between two kernels of the step
-        # delays the next one by a few microseconds).
-        pst = [[ev() for _ in range(4)] for _ in range(ps)]
-        for s in range(ps):
-            layers[s % L].prefill(xp[s % L], stage_events=pst[s])
-        torch.cuda.synchronize()
-        gu_ms_p = sum(pst[s][0].elapsed_time(pst[s][1]) for s in range(ps)) / ps
-        dn_ms_p = sum(pst[s][1].elapsed_time(pst[s][2]) for s in range(ps)) / ps
-        cb_ms_p = sum(pst[s][2].elapsed_time(pst[s][3]) for s in range(ps)) / ps
-        p0, p1 = ev(), ev()
-        p0.record()
-        for s in range(ps):
-            layers[s % L].prefill(xp[s % L])
-        p1.record()
-        torch.cuda.synchronize()
-        pms = p0.elapsed_time(p1) / ps
-        pairs = pT * K
-        flops = 6 * H * I * pairs + 2 * pT * H * E
-        gu_flops = 4 * H * I * pairs
-        pbytes = E * bpe + E * H * 2 + 2 * pT * H * 2
-        gu_tf = gu_flops / (gu_ms_p * 1e-3) / 1e12
-        t_min = max(pbytes / (HBM_PEAK_GBS * 1e9), flops / (MXFP4_PEAK_TFLOPS * 1e12))
-        prefill = {
-            "value": pT / (pms * 1e-3), "unit": "tokens/s", "ms_per_step": pms, "tokens": pT,
-            "steps": ps, "settle_steps": p_settled, "algorithmic_flops": flops,
-            "algorithmic_bytes": pbytes,
-            "layer_TFLOPs": flops / (pms * 1e-3) / 1e12,
-            "layer_frac_mxfp4_peak": flops / (pms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS,
-            "layer_frac_binding_roofline": t_min / (pms * 1e-3),
-            "kernel_ms": {"gate_up": gu_ms_p, "down": dn_ms_p, "combine": cb_ms_p,
-                          "router+mapping": pms - gu_ms_p - dn_ms_p - cb_ms_p},
-            "roofline": {"bound": "mfma", "kernel": "prefill_gemm_kernel<gate_up>",
-                         "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": gu_tf / BF16_PEAK_TFLOPS,
-                         "frac_of_mxfp4_peak": gu_tf / MXFP4_PEAK_TFLOPS,
-                         "traffic": traffic_pre, "traffic_source": traffic_src,
-                         "algorithmic_flops_per_launch": gu_flops, "avg_launch_ms": gu_ms_p},
-        }
+        prefill = time_prefill(layers, xp, shape, args.prefill_steps, args.settle)
+        gu_ms_p = prefill["kernel_ms"]["gate_up"]
+        gu_flops = prefill.pop("gate_up_algorithmic_flops")
+        gu_tf = prefill["gate_up_TFLOPs"]
+        prefill["roofline"] = {"bound": "mfma", "kernel": "prefill_gemm_kernel<gate_up>",
+                               "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                               "frac": gu_tf / BF16_PEAK_TFLOPS,
+                               "frac_of_mxfp4_peak": gu_tf / MXFP4_PEAK_TFLOPS,
+                               "traffic": traffic_pre, "traffic_source": traffic_src,
+                               "algorithmic_flops_per_launch": gu_flops, "avg_launch_ms": gu_ms_p}
+        del xp
+    del layers, xs
+    torch.cuda.empty_cache()
+
+    others = None
+    if not args.no_other_configs and args.workload == "gptoss120b":
+        others = other_configs(dev, gen, min(args.settle, 0.15))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -522,6 +697,7 @@ def main():
         "cpu_baseline": None if cpu is None else cpu["decode"],
         "decode": decode,
         "prefill": prefill,
+        "other_configs": others,
     }
     print(json.dumps(out))
 

@@ -83,6 +83,11 @@ class RefLayer:
         self.dn_bias = lt.down_bias
         self.router_w = lt.router_w
         self.router_b = lt.router_b
+        self._set_activation()
+
+    def _set_activation(self):
+        """GPT-OSS's call (model_bf16.py:1359-1386): Swish, gate <= limit, up in
+        [-limit + 1, limit + 1]; plain SwiGLU (no limit): SiLU, no clamps."""
         if self.limit is None:
             self.act = moe_cte.SILU
             self.clamps = dict(gate_clamp_upper_limit=None, gate_clamp_lower_limit=None,
@@ -92,6 +97,24 @@ class RefLayer:
             self.clamps = dict(gate_clamp_upper_limit=self.limit, gate_clamp_lower_limit=None,
                                up_clamp_upper_limit=self.limit + 1,
                                up_clamp_lower_limit=-self.limit + 1)
+
+    @classmethod
+    def from_dense(cls, gate_up, down, gu_bias, dn_bias, router_w, router_b, top_k,
+                   swiglu_limit):
+        """A layer from bf16 parameters as the reference's CPU model holds them
+        (weight_loaders_bf16.py:319-488 outputs): gate_up [E, H, 2I] = [gate | up], down
+        [E, I, H], gate_up bias [E, 2I] (up half with its +1), down bias [E, H], router
+        weight [E, H]."""
+        self = cls.__new__(cls)
+        self.gate_up, self.down = gate_up, down
+        self.E, self.H, twoI = gate_up.shape
+        self.I = twoI // 2
+        self.gu_bias, self.dn_bias = gu_bias, dn_bias
+        self.router_w, self.router_b = router_w, router_b
+        self.K, self.limit, self.lazy = top_k, swiglu_limit, False
+        self.shape = None
+        self._set_activation()
+        return self
 
     # ---- routing (router.py torch flow, fp32)
     def route(self, x: torch.Tensor):
