@@ -220,6 +220,33 @@ int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked, const uint8
                   void* stream);
 
 /*
+ * Whole prefill expert layer in one call: router on x, blockwise mapping (block_size),
+ * then the mxmoe_moe_cte pipeline with POST_SCALE.  The counterpart of the call sequence
+ * of the GPT-OSS MXFP4 prefill layer, vllm_neuron/model/gpt_oss/model_mxfp4.py:1337-1433
+ * (NF.router -> NF.build_blockwise_mapping -> NF.moe_cte shard_on_block_mx, skip_token)
+ * for an already-normalized input on one rank holding every expert.
+ * Router arguments as mxmoe_router_topk (router_compute_dtype is its compute_dtype;
+ * x is bf16); the logits are bit-identical to its.  padding_mask uint8 [T] or NULL as
+ * mxmoe_blockwise_mapping; the mapping equals its result.  Weights, biases, act,
+ * clamps, out_f32 and out as mxmoe_moe_cte (weight_fmt MXMOE_WFMT_MXFP4 or
+ * MXMOE_WFMT_MXFP8).
+ * stage_events: NULL, or 5 hipEvent_t recorded before the router, after the mapping
+ * (before the gate_up GEMM), after the gate_up GEMM, after the down GEMM and after the
+ * combine.
+ */
+size_t mxmoe_moe_prefill_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                                         int64_t block_size);
+int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int router_w_dtype,
+                      const void* router_b, int router_b_dtype, int router_act,
+                      int act_before_topk, int renorm, float renorm_eps, int router_compute_dtype,
+                      const uint8_t* padding_mask, const uint8_t* gu_q, const uint8_t* gu_s,
+                      const uint8_t* dn_q, const uint8_t* dn_s, int weight_fmt,
+                      const uint16_t* gu_bias, const uint16_t* dn_bias, int64_t T, int64_t H,
+                      int64_t I, int64_t E, int top_k, int64_t block_size, int act,
+                      const float* clamps, int out_f32, void* out, void* workspace,
+                      size_t workspace_bytes, void* const* stage_events, void* stream);
+
+/*
  * Decode expert MLP given routing: weight-streaming grouped GEMMs over the selected
  * experts only, fp32 intermediates (the down GEMM consumes a hi/lo bf16 split of
  * the fp32 activations), ascending-expert fp32 combine, bf16 output.

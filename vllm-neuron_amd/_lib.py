@@ -46,6 +46,10 @@ _SIGNATURES = {
     "mxmoe_moe_cte_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_cte": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                            _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _SZ, _P, _P]),
+    "mxmoe_moe_prefill_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I, _I64]),
+    "mxmoe_moe_prefill": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _I, _P,
+                               _P, _I64, _I64, _I64, _I64, _I, _I64, _I, _P, _I, _P, _P, _SZ, _P,
+                               _P]),
     "mxmoe_moe_tkg_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
     "mxmoe_moe_tkg": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P,
                            _I, _P, _P, _SZ, _P, _P]),

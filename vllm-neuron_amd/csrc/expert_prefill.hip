@@ -731,95 +731,6 @@ __global__ void __launch_bounds__(kPThreads)
     prefill_run<F, GATE_UP, 8, false>(stage, nullptr, args, p, stok, m0, e, rg_first);
 }
 
-// The GEMMs schedule M-tiles in groups of G consecutive tiles of one block (G = the
-// largest power of two up to 16 dividing B / 128): the group's workgroups run one after
-// another on one XCD, so a block's second, mostly empty M-tile reads the weight rows
-// while the first one's workgroups hold them in L2.
-constexpr int kMaxGroupTiles = 16;
-inline int prefill_group_tiles(int64_t block_size) {
-  const int64_t per = block_size / kPM;
-  int g = 1;
-  while (g < kMaxGroupTiles && per % (2 * g) == 0) g *= 2;
-  return g;
-}
-
-// order[r] = (first M-tile of the r-th group by descending weight, ties in M order; the
-// group's expert).  The weight of a tile is the number of its 16-slot subtiles whose
-// first slot holds a real token (the GEMM's subtile count when real slots come first,
-// as the blockwise mapping lays them out; a different layout only changes the
-// schedule), a group's the sum over its tiles.  One workgroup: a histogram of the
-// weights, then a stable scatter ranked by ballots per weight.
-constexpr int kOrderThreads = 1024;
-constexpr int kMaxWeights = kMaxGroupTiles * (kPM / 16) + 1;
-constexpr int kOrderMaxTiles = 10240;  // 5 B of LDS per M-tile (with the sort tables < 64 KiB)
-__device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
-  int w = 0;
-#pragma unroll
-  for (int s = 0; s < kPM / 16; ++s) {
-    const int tk = tp2id[(size_t)mt * kPM + 16 * s];
-    w += (tk >= 0 && tk < T) ? 1 : 0;
-  }
-  return w;
-}
-
-constexpr int kOrderWaves = kOrderThreads / 64;
-struct OrderLds {
-  int hist[kMaxWeights];
-  int next[kMaxWeights];  // next free rank per weight
-  int cnt[kOrderWaves][kMaxWeights];
-};
-
-// One sort over the tile weights and experts staged in LDS (s_w, s_e).
-__device__ void order_pass(const uint8_t* s_w, const int32_t* s_e, int n_groups, int G,
-                           int2* __restrict__ order, OrderLds& L) {
-  const int NW = G * (kPM / 16) + 1;  // weights 0 .. 8G
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  auto weight = [&](int g) {
-    int w = 0;
-    for (int i = 0; i < G; ++i) w += s_w[g * G + i];
-    return w;
-  };
-  for (int v = tid; v < NW; v += kOrderThreads) L.hist[v] = 0;
-  __syncthreads();
-  for (int base = 0; base < n_groups; base += kOrderThreads) {
-    const int g = base + tid;
-    if (g < n_groups) atomicAdd(&L.hist[weight(g)], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int r = 0;
-    for (int w = NW - 1; w >= 0; --w) {
-      L.next[w] = r;
-      r += L.hist[w];
-    }
-  }
-  __syncthreads();
-  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < n_groups; base += kOrderThreads) {
-    const int g = base + tid;
-    const int w = g < n_groups ? weight(g) : -1;
-    int in_wave = 0;
-    for (int v = 0; v < NW; ++v) {
-      const unsigned long long m = __ballot(w == v);
-      if (lane == 0) L.cnt[wave][v] = __popcll(m);
-      if (w == v) in_wave = __popcll(m & below);
-    }
-    __syncthreads();
-    if (w >= 0) {
-      int r = L.next[w] + in_wave;
-      for (int j = 0; j < wave; ++j) r += L.cnt[j][w];
-      order[r] = int2{g * G, s_e[g * G]};
-    }
-    __syncthreads();
-    for (int v = tid; v < NW; v += kOrderThreads) {
-      int c = 0;
-      for (int j = 0; j < kOrderWaves; ++j) c += L.cnt[j][v];
-      L.next[v] += c;
-    }
-    __syncthreads();
-  }
-}
-
 // The order of the groups of G M-tiles both GEMMs run.  The tiles' weights and experts
 // are read once into LDS (dynamic: 5 B per tile).
 __global__ void __launch_bounds__(kOrderThreads) cte_tile_order_kernel(
@@ -1209,17 +1120,16 @@ extern "C" size_t mxmoe_moe_cte_workspace_bytes(int64_t T, int64_t H, int64_t I,
   return cte_carve(nullptr, ~(size_t)0, T, H, I, E, block_size * n_blocks, scale_mode, nullptr);
 }
 
-extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
-                             const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
-                             const uint8_t* dn_s, int weight_fmt, const uint16_t* gu_bias,
-                             const uint16_t* dn_bias, const uint16_t* expert_const,
-                             const int32_t* token_position_to_id,
-                             const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
-                             int64_t T, int64_t H, int64_t I, int64_t E, int act,
-                             const float* clamps, int scale_mode, int out_f32, void* out,
-                             void* workspace, size_t workspace_bytes, void* const* stage_events,
-                             void* stream) {
-  clear_error();
+namespace mxmoe {
+
+int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu_q,
+            const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s, int weight_fmt,
+            const uint16_t* gu_bias, const uint16_t* dn_bias, const uint16_t* expert_const,
+            const int32_t* token_position_to_id, const int32_t* block_to_expert,
+            int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I, int64_t E,
+            int act, const float* clamps, int scale_mode, int out_f32, void* out,
+            void* workspace, size_t workspace_bytes, void* const* stage_events,
+            const int2* order_pre, hipStream_t s) {
   const bool bf16w = weight_fmt == MXMOE_WFMT_BF16;
   MXMOE_REQUIRE(x && affinities_masked && gu_q && dn_q && (bf16w || (gu_s && dn_s)) &&
                     token_position_to_id && block_to_expert && out && workspace,
@@ -1255,7 +1165,6 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   CteWs w;
   cte_carve(workspace, workspace_bytes, T, H, I, E, n_slots, scale_mode, &w);
   const bool pre = scale_mode == MXMOE_SCALE_PRE, delayed = scale_mode == MXMOE_SCALE_PRE_DELAYED;
-  hipStream_t s = as_stream(stream);
   auto mark = [&](int i) {
     mark_event(stage_events, i, s);
   };
@@ -1268,7 +1177,7 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.B = (int)block_size;
   a.n_mtiles = (int)(n_slots / kPM);
   a.group = prefill_group_tiles(block_size);
-  a.order = w.order;
+  a.order = order_pre ? order_pre : w.order;
   a.E = (int)E;
   a.a_by_slot = pre ? 1 : 0;
   a.inv = w.inv;
@@ -1291,9 +1200,10 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
   a.K = (int)H;
   a.N_rows = (int)(2 * I);
   a.n_ntiles = bf16w ? prefill_ntiles_bf16(true, I, H) : prefill_ntiles(2 * I, weight_fmt);
-  hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
-                     (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
-                     (int)block_size, a.n_mtiles, a.group, (int)T, w.order);
+  if (!order_pre)
+    hipLaunchKernelGGL(cte_tile_order_kernel, dim3(1), dim3(kOrderThreads),
+                       (size_t)a.n_mtiles * 5, s, token_position_to_id, block_to_expert,
+                       (int)block_size, a.n_mtiles, a.group, (int)T, w.order);
   mark(0);
   if (bf16w)
     launch_prefill_gemm_bf16(true, a, s);
@@ -1333,6 +1243,25 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
                        (int)H, (int)E, scale_mode, out_f32, out);
   mark(3);
   return check_launch("moe_cte");
+}
+
+}  // namespace mxmoe
+
+extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
+                             const uint8_t* gu_q, const uint8_t* gu_s, const uint8_t* dn_q,
+                             const uint8_t* dn_s, int weight_fmt, const uint16_t* gu_bias,
+                             const uint16_t* dn_bias, const uint16_t* expert_const,
+                             const int32_t* token_position_to_id,
+                             const int32_t* block_to_expert, int64_t n_blocks, int64_t block_size,
+                             int64_t T, int64_t H, int64_t I, int64_t E, int act,
+                             const float* clamps, int scale_mode, int out_f32, void* out,
+                             void* workspace, size_t workspace_bytes, void* const* stage_events,
+                             void* stream) {
+  clear_error();
+  return cte_run(x, affinities_masked, gu_q, gu_s, dn_q, dn_s, weight_fmt, gu_bias, dn_bias,
+                 expert_const, token_position_to_id, block_to_expert, n_blocks, block_size, T, H,
+                 I, E, act, clamps, scale_mode, out_f32, out, workspace, workspace_bytes,
+                 stage_events, nullptr, as_stream(stream));
 }
 
 extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, const uint8_t* ws,

@@ -10,11 +10,10 @@
 // are scattered.  No step depends on atomic ordering, so the result is unique.
 #include "capi_util.h"
 #include "common.h"
+#include "permute_dev.h"
 
 namespace mxmoe {
 
-constexpr int kChunkTok = 64;
-constexpr int kMaxE = 1024;
 constexpr int kBwThreads = 256;
 
 // Calls f(e, a) for the nonzero affinities of row t handled by thread quarter q
@@ -65,71 +64,15 @@ __global__ void __launch_bounds__(kBwThreads) bw_count_kernel(
   }
 }
 
-// Pass 2 (one workgroup of 1024 threads): per-expert exclusive prefix over chunks (wave
-// per expert), block counts, block offsets, block_to_expert, conditions.
+// Pass 2 (one workgroup of 1024 threads): per-expert exclusive prefix over chunks, block
+// counts, block offsets, block_to_expert, conditions (bw_scan_body).
 __global__ void __launch_bounds__(1024) bw_scan_kernel(
     int32_t* __restrict__ counts, int n_chunks, int E, int B, int N,
     int32_t* __restrict__ expert_pos, int32_t* __restrict__ block_to_expert,
     int32_t* __restrict__ conditions, int32_t* __restrict__ expert_counts) {
-  __shared__ int cum[kMaxE];  // per-expert totals, then inclusive cumulative blocks
-  __shared__ int wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = wave; e < E; e += 16) {
-    int32_t* ce = counts + (size_t)e * n_chunks;
-    int run = 0;
-    for (int c0 = 0; c0 < n_chunks; c0 += 64) {
-      const int c = c0 + lane;
-      const int v = c < n_chunks ? ce[c] : 0;
-      int x = v;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int o = __shfl_up(x, off);
-        if (lane >= off) x += o;
-      }
-      if (c < n_chunks) ce[c] = run + x - v;  // exclusive prefix within the expert
-      run += __shfl(x, 63);
-    }
-    if (lane == 0) cum[e] = run;
-  }
-  __syncthreads();
-  const int e = tid;
-  int total = 0, nb = 0;
-  if (e < E) {
-    total = cum[e];
-    nb = (total + B - 1) / B;
-    if (expert_counts) expert_counts[e] = total;
-  }
-  __syncthreads();
-  // Inclusive block scan over experts: wave scan, then across waves.
-  int v = nb;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(v, off);
-    if (lane >= off) v += o;
-  }
-  if (lane == 63) wsum[wave] = v;
-  __syncthreads();
-  int pre = 0;
-  for (int w = 0; w < wave; ++w) pre += wsum[w];
-  v += pre;
-  if (e < E) {
-    cum[e] = v;
-    expert_pos[e] = (v - nb) * B;  // first slot of the expert's run
-  }
-  __syncthreads();
-  const int used = cum[E - 1];
-  for (int n = tid; n < N; n += 1024) {
-    // block_to_expert[n] = #{e < E-1 : n >= cum[e]}  (cum is non-decreasing)
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (cum[mid] <= n) lo = mid + 1;
-      else hi = mid;
-    }
-    block_to_expert[n] = lo;
-    // A block inside a run holds at least one token; blocks past the runs are empty.
-    conditions[n] = n < used ? 1 : 0;
-  }
+  __shared__ int cum[kMaxE], tot[kMaxE], wsum[16];
+  bw_scan_body(counts, n_chunks, E, B, N, expert_pos, block_to_expert, conditions,
+               expert_counts, cum, tot, wsum);
 }
 
 // Pass 3: scatter token ids.  token_position_to_id was filled with -1 by pass 1.

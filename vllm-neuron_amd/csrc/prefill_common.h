@@ -85,6 +85,95 @@ __device__ __forceinline__ bool prefill_tile_begin(const PrefillArgs& args, int3
   return true;
 }
 
+// The GEMMs schedule M-tiles in groups of G consecutive tiles of one block (G = the
+// largest power of two up to 16 dividing B / 128): the group's workgroups run one after
+// another on one XCD, so a block's second, mostly empty M-tile reads the weight rows
+// while the first one's workgroups hold them in L2.
+constexpr int kMaxGroupTiles = 16;
+inline int prefill_group_tiles(int64_t block_size) {
+  const int64_t per = block_size / kPM;
+  int g = 1;
+  while (g < kMaxGroupTiles && per % (2 * g) == 0) g *= 2;
+  return g;
+}
+
+// order[r] = (first M-tile of the r-th group by descending weight, ties in M order; the
+// group's expert).  The weight of a tile is the number of its 16-slot subtiles whose
+// first slot holds a real token (the GEMM's subtile count when real slots come first,
+// as the blockwise mapping lays them out; a different layout only changes the
+// schedule), a group's the sum over its tiles.  One workgroup: a histogram of the
+// weights, then a stable scatter ranked by ballots per weight.
+constexpr int kOrderThreads = 1024;
+constexpr int kMaxWeights = kMaxGroupTiles * (kPM / 16) + 1;
+constexpr int kOrderMaxTiles = 10240;  // 5 B of LDS per M-tile (with the sort tables < 64 KiB)
+__device__ __forceinline__ int tile_weight(const int32_t* __restrict__ tp2id, int mt, int T) {
+  int w = 0;
+#pragma unroll
+  for (int s = 0; s < kPM / 16; ++s) {
+    const int tk = tp2id[(size_t)mt * kPM + 16 * s];
+    w += (tk >= 0 && tk < T) ? 1 : 0;
+  }
+  return w;
+}
+
+constexpr int kOrderWaves = kOrderThreads / 64;
+struct OrderLds {
+  int hist[kMaxWeights];
+  int next[kMaxWeights];  // next free rank per weight
+  int cnt[kOrderWaves][kMaxWeights];
+};
+
+// One sort over the tile weights and experts staged in LDS (s_w, s_e).
+__device__ inline void order_pass(const uint8_t* s_w, const int32_t* s_e, int n_groups, int G,
+                           int2* __restrict__ order, OrderLds& L) {
+  const int NW = G * (kPM / 16) + 1;  // weights 0 .. 8G
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto weight = [&](int g) {
+    int w = 0;
+    for (int i = 0; i < G; ++i) w += s_w[g * G + i];
+    return w;
+  };
+  for (int v = tid; v < NW; v += kOrderThreads) L.hist[v] = 0;
+  __syncthreads();
+  for (int base = 0; base < n_groups; base += kOrderThreads) {
+    const int g = base + tid;
+    if (g < n_groups) atomicAdd(&L.hist[weight(g)], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int r = 0;
+    for (int w = NW - 1; w >= 0; --w) {
+      L.next[w] = r;
+      r += L.hist[w];
+    }
+  }
+  __syncthreads();
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < n_groups; base += kOrderThreads) {
+    const int g = base + tid;
+    const int w = g < n_groups ? weight(g) : -1;
+    int in_wave = 0;
+    for (int v = 0; v < NW; ++v) {
+      const unsigned long long m = __ballot(w == v);
+      if (lane == 0) L.cnt[wave][v] = __popcll(m);
+      if (w == v) in_wave = __popcll(m & below);
+    }
+    __syncthreads();
+    if (w >= 0) {
+      int r = L.next[w] + in_wave;
+      for (int j = 0; j < wave; ++j) r += L.cnt[j][w];
+      order[r] = int2{g * G, s_e[g * G]};
+    }
+    __syncthreads();
+    for (int v = tid; v < NW; v += kOrderThreads) {
+      int c = 0;
+      for (int j = 0; j < kOrderWaves; ++j) c += L.cnt[j][v];
+      L.next[v] += c;
+    }
+    __syncthreads();
+  }
+}
+
 // Round to bf16 (nearest even) and back: the gfx950 conversion instruction, which
 // gives round_bf16's result on every non-NaN input (NaN stays NaN).
 __device__ __forceinline__ float rb(float v) { return (float)(__bf16)v; }
@@ -132,5 +221,17 @@ void launch_prefill_gemm_bf16(bool gate_up, const PrefillArgs& a, hipStream_t s)
 void launch_decode_gemm_bf16(bool gate_up, const PrefillArgs& a, const uint16_t* a_lo,
                              uint16_t* out_lo, float* y32, hipStream_t s);
 int prefill_ntiles_bf16(bool gate_up, int64_t I, int64_t H);
+
+// The moe_cte flow (expert_prefill.hip): gate_up GEMM, down GEMM, combine over a blockwise
+// mapping.  order_pre: the M-tile groups' schedule already computed (the fused prefill
+// router writes it); null: computed from the mapping first.
+int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu_q,
+            const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s, int weight_fmt,
+            const uint16_t* gu_bias, const uint16_t* dn_bias, const uint16_t* expert_const,
+            const int32_t* token_position_to_id, const int32_t* block_to_expert,
+            int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I, int64_t E,
+            int act, const float* clamps, int scale_mode, int out_f32, void* out,
+            void* workspace, size_t workspace_bytes, void* const* stage_events,
+            const int2* order_pre, hipStream_t s);
 
 }  // namespace mxmoe

@@ -26,85 +26,8 @@ __global__ void __launch_bounds__(64 * NW) router_logits_kernel(
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int q = lane >> 4, r16 = lane & 15;
   const int t0 = blockIdx.x * 16 * TT, e0 = blockIdx.y * 16 * ET;
-  const int nc = (H + 127) / 128;
-  const int tail_q = (H % 128) / 32;  // blocks of 32 in a partial last chunk
-
-  const uint16_t* xr[TT];
-  const uint16_t* wr[ET];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) xr[t] = x + (size_t)min(t0 + 16 * t + r16, T - 1) * H;
-#pragma unroll
-  for (int e = 0; e < ET; ++e) wr[e] = w + (size_t)min(e0 + 16 * e + r16, E - 1) * H;
-
   f32x4 acc[ET][TT];
-#pragma unroll
-  for (int e = 0; e < ET; ++e)
-#pragma unroll
-    for (int t = 0; t < TT; ++t) acc[e][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  // Chunk c's operands (lanes past K in a partial last chunk feed zeros; every lane runs
-  // the MFMAs), loaded one chunk ahead of their MFMAs into the other register set.
-  auto load = [&](int c, u32x4 (&xv)[TT][4], u32x4 (&wv)[ET][4]) {
-    const bool ok = (c < H / 128) || (q < tail_q);
-    const int k0 = c * 128 + q * 32;
-#pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        xv[t][j] = ok ? *reinterpret_cast<const u32x4*>(xr[t] + k0 + 8 * j) : zero4;
-#pragma unroll
-    for (int e = 0; e < ET; ++e)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wv[e][j] = ok ? *reinterpret_cast<const u32x4*>(wr[e] + k0 + 8 * j) : zero4;
-  };
-  auto mma = [&](const u32x4 (&xv)[TT][4], const u32x4 (&wv)[ET][4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < ET; ++e) {
-        if constexpr (OP == kOpF16) {
-          f16x8 a;
-          if constexpr (WF16) a = __builtin_bit_cast(f16x8, wv[e][j]);
-          else a = bf16x8_to_f16x8(wv[e][j]);
-#pragma unroll
-          for (int t = 0; t < TT; ++t) {
-            f16x8 b;
-            if constexpr (XF16) b = __builtin_bit_cast(f16x8, xv[t][j]);
-            else b = bf16x8_to_f16x8(xv[t][j]);
-            acc[e][t] = mfma16_f16(a, b, acc[e][t]);
-          }
-        } else if constexpr (OP == kOpExact) {
-          static_assert(WF16 && !XF16, "exact mode splits fp16 weights against bf16 x");
-          bf16x8 hi, lo;
-          f16x8_split_bf16(wv[e][j], hi, lo);
-#pragma unroll
-          for (int t = 0; t < TT; ++t) {
-            acc[e][t] = mfma16(hi, as_bf16x8(xv[t][j]), acc[e][t]);
-            acc[e][t] = mfma16(lo, as_bf16x8(xv[t][j]), acc[e][t]);
-          }
-        } else {
-          static_assert(!XF16, "bf16 MFMA takes bf16 x");
-          bf16x8 a;
-          if constexpr (WF16) a = f16x8_to_bf16x8(wv[e][j]);
-          else a = as_bf16x8(wv[e][j]);
-#pragma unroll
-          for (int t = 0; t < TT; ++t) acc[e][t] = mfma16(a, as_bf16x8(xv[t][j]), acc[e][t]);
-        }
-      }
-  };
-  u32x4 xa[TT][4], wa[ET][4], xb[TT][4], wb[ET][4];
-  int c = wave;
-  if (c < nc) load(c, xa, wa);
-  for (; c < nc; c += 2 * NW) {
-    const int c1 = c + NW;
-    if (c1 < nc) load(c1, xb, wb);
-    mma(xa, wa);
-    if (c1 >= nc) break;
-    if (c1 + NW < nc) load(c1 + NW, xa, wa);
-    mma(xb, wb);
-  }
+  router_partial_logits<TT, ET, NW, XF16, WF16, OP>(x, w, T, H, E, t0, e0, wave, acc);
 #pragma unroll
   for (int e = 0; e < ET; ++e)
 #pragma unroll

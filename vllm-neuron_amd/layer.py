@@ -60,6 +60,49 @@ class MXFP4MoE:
 
     def prefill(self, x: torch.Tensor, padding_mask: Optional[torch.Tensor] = None,
                 output_dtype: torch.dtype = torch.bfloat16, stage_events=None):
+        """Router, blockwise mapping and moe_cte in one library call (mxmoe_moe_prefill):
+        the result of ``prefill_ops`` bit for bit, in four launches before the GEMMs
+        instead of seven.  The workspace is cached per token count, so calls of one layer
+        object belong on one stream.  stage_events: optional 5 torch.cuda.Event
+        (enable_timing) recorded before the router, before the gate_up GEMM, after it,
+        after the down GEMM and after the combine."""
+        if output_dtype not in (torch.bfloat16, torch.float32):
+            raise NotImplementedError("output_dtype must be bfloat16 or float32")
+        w = self.w
+        T, H = x.shape
+        dev = _lib.require_cuda(x, w.gu_q)
+        if x.dtype != torch.bfloat16 or H != w.H:
+            raise ValueError(f"expected bf16 [T, {w.H}] hidden states")
+        pm = None
+        if padding_mask is not None:
+            pm = padding_mask.reshape(-1).to(device=dev, dtype=torch.uint8).contiguous()
+            if pm.numel() != T:
+                raise ValueError(f"padding_mask has {pm.numel()} entries, expected {T}")
+        L = _lib.lib()
+        key = ("prefill", T)
+        ws = self._ws.get(key)
+        if ws is None:
+            ws = _lib.workspace(L.mxmoe_moe_prefill_workspace_bytes(T, H, w.I, w.E, self.top_k,
+                                                                    self.block_size), dev)
+            self._ws[key] = ws
+        x = x.contiguous()
+        out = torch.empty(T, H, dtype=output_dtype, device=dev)
+        rc = L.mxmoe_moe_prefill(
+            x.data_ptr(), self.router_w.data_ptr(), self._w_dt, _lib.ptr(self.router_b),
+            self._b_dt, _lib.ROUTER_SOFTMAX, 0, 0, 0.0, _lib.DT_F32, _lib.ptr(pm),
+            w.gu_q.data_ptr(), w.gu_s.data_ptr(), w.dn_q.data_ptr(), w.dn_s.data_ptr(),
+            _lib.WFMT_MXFP4, _lib.ptr(w.gu_bias), _lib.ptr(w.dn_bias), T, H, w.I, w.E, self.top_k,
+            self.block_size, self.act, self._clamps, int(output_dtype == torch.float32),
+            out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.event_array(stage_events),
+            _lib.stream_handle(dev))
+        _lib.check(rc, "mxmoe_moe_prefill")
+        return out
+
+    def prefill_ops(self, x: torch.Tensor, padding_mask: Optional[torch.Tensor] = None,
+                    output_dtype: torch.dtype = torch.bfloat16, stage_events=None):
+        """The prefill as the reference model calls the operators (model_bf16.py:1282-1413):
+        router, build_blockwise_mapping, moe_cte, each its own library call.
+        stage_events: optional 4 events around the moe_cte GEMMs and combine."""
         aff, _, _, _ = self.route(x)
         aff_m, tp2id, b2e, _ = build_blockwise_mapping(aff, self.E, self.top_k, self.block_size,
                                                        padding_mask=padding_mask)
