@@ -3,18 +3,20 @@
 //
 // The separate operator calls take seven dependent launches before the first GEMM
 // (router logits, top-k, mapping count / scan / scatter, tile order) and the router
-// logits read their operands in 32-token x 64-expert tiles.  Here four launches do it:
+// logits read their operands in 32-token x 64-expert tiles.  Here three launches do it:
 //   pf_logits_kernel   workgroup = 64 tokens x 64 ETW experts x one quarter of K (the
 //                      128-wide chunks q, q + 4, ...), operands staged through LDS once
-//                      per workgroup; writes fp32 partial sums part[q][T][E];
-//   pf_topk_kernel     one workgroup per 64-token chunk: partial sums added in the order
-//                      0..3, bias, top-k and activation per token (16 lanes per token), the
-//                      masked affinities, the chunk's per-expert token masks and counts;
-//                      fills token_position_to_id with -1;
-//   pf_scan_order_kernel  one workgroup: the mapping's scan (bw_scan_body) and the
-//                      schedule of the GEMMs' M-tile groups, whose weights follow from
-//                      the per-expert counts (a block's real slots come first);
-//   pf_scatter_kernel  the routed pairs' slots.
+//                      per workgroup; writes fp32 partial sums part[q][T][E] and clears the
+//                      64-token chunk masks;
+//   pf_topk_kernel     a wave per token: partial sums added in the order 0..3, bias,
+//                      top-k and activation, the masked affinities, the token's bits in
+//                      its chunk's per-expert masks (global atomic OR); fills
+//                      token_position_to_id with -1;
+//   pf_place_kernel    a workgroup per 64-token chunk: each derives the per-expert totals
+//                      and its chunk's prefix from all masks and places its chunk's pairs;
+//                      workgroup 0 also writes block_to_expert and the schedule of the GEMMs'
+//                      M-tile groups, whose weights follow from the totals (a block's real
+//                      slots come first).
 // The logits are the router kernel's (router.hip) bit for bit: the same K quarters, the
 // same MFMA sequence per accumulator, the quarters summed in the same order.  The mapping
 // and schedule equal mxmoe_blockwise_mapping's and cte_tile_order_kernel's.
@@ -32,9 +34,9 @@ namespace mxmoe {
 
 constexpr int kPfParts = 4;    // K quarters (the router kernel's four waves)
 constexpr int kPfTok = 64;     // tokens per logits workgroup and per mapping chunk
-// M-tiles one call schedules: the schedule kernel's LDS (5 B per tile next to the scan's
-// 17.5 KB of tables) stays under 64 KiB.
-constexpr int kPfMaxTiles = 8192;
+// M-tiles one call schedules: the placement kernel's LDS (5 B per tile next to 25.3 KB of
+// tables) stays under 64 KiB.
+constexpr int kPfMaxTiles = 7168;
 template <int N>
 using IntC = std::integral_constant<int, N>;
 static_assert(kPfTok == kChunkTok, "a logits tile is one mapping chunk");
@@ -45,11 +47,13 @@ static_assert(kPfTok == kChunkTok, "a logits tile is one mapping chunk");
 // router_partial_logits' wave kp.  Workgroup: 64 tokens (4 tiles of 16) x 64 ETW experts;
 // wave w takes expert tiles ETW w .. ETW w + ETW - 1 against all 64 tokens.  A chunk's
 // rows (16-byte blocks XOR-swizzled by row) go global -> registers -> LDS, one chunk
-// ahead, through two stages; one barrier per chunk.
+// ahead, through two stages; one barrier per chunk.  The workgroups of expert tile 0 and
+// part 0 also clear their token tile's chunk masks (64 bits per expert).
 template <int ETW, bool XF16, bool WF16, int OP>
 __global__ void __launch_bounds__(256) pf_logits_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ w, int T,
-                                                        int H, int E, float* __restrict__ part) {
+                                                        int H, int E, float* __restrict__ part,
+                                                        unsigned long long* __restrict__ masks) {
   constexpr int TT = kPfTok / 16;
   constexpr int WR = 64 * ETW;                   // router rows per workgroup
   constexpr int XB = kPfTok * 16 / 256, WB = WR * 16 / 256;  // 16-B blocks per thread
@@ -60,6 +64,9 @@ __global__ void __launch_bounds__(256) pf_logits_kernel(const uint16_t* __restri
   const int t0 = blockIdx.x * kPfTok, e0 = blockIdx.y * WR, kp = blockIdx.z;
   const int nc = (H + 127) / 128;
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  // The top-k kernel ORs token bits into the chunk masks: clear this token tile's.
+  if (blockIdx.y == 0 && kp == 0)
+    for (int i = tid; i < E; i += 256) masks[(size_t)blockIdx.x * E + i] = 0ull;
 
   // The part's chunks kp, kp + 4, ... go global -> registers through a ring of D slots,
   // D chunks ahead (chunk indices past the part re-read its last chunk, never computed),
@@ -210,158 +217,175 @@ __global__ void __launch_bounds__(256) pf_logits_kernel(const uint16_t* __restri
     }
 }
 
-// One workgroup of 16 waves per 64-token chunk c; wave w takes tokens 64 c + 4 w + u,
-// u < 4.  Per token: the logits as the router kernel forms them (partial sums 0..3 in
-// order, plus the bias rounded to bias_rnd, the sum rounded to logit_rnd), top-k and
-// activation (topk_row_group), the masked affinity row aff_m[t] (a * padding_mask, as
-// bw_count_kernel writes it), sel[t][k] = the k-th selected expert if its affinity is
-// nonzero, else -1; each nonzero affinity sets the token's bit in its expert's mask.  Then
-// the chunk's masks and counts (counts expert-major), as bw_count_kernel writes them.
-// W = 16: a row of 16 lanes per token (lane j holds experts j, j + 16, ...), the wave's
-// four tokens at once; W = 64: the whole wave per token (lane l holds experts l, l + 64,
-// ...), one token after the other, as the router kernel's top-k.  Both select and weight
-// identically except a softmax over all E logits before the top-k, whose sum runs in a
-// different order over 16 lanes: that case, and E > 256, take W = 64.  P: values per lane.
-template <int W, int P>
-__global__ void __launch_bounds__(1024) pf_topk_kernel(
+// Top-k of 4 tokens per workgroup, one token per wave (lane l holds experts l, l + 64, ...;
+// topk_row_wave, as the router kernel's top-k): the selection is VALU latency-bound, and
+// four waves per SIMD hide it (16-lane rows with four tokens per wave and one wave per SIMD
+// measured 11.3 against 9.4 us at 4,096 tokens and 128 experts).  Per token: the logits as
+// the router kernel forms them (partial sums 0..3 in order, plus the bias rounded to
+// bias_rnd, the sum rounded to logit_rnd), top-k and activation, the masked affinity row
+// aff_m[t] (a * padding_mask, as bw_count_kernel writes it), sel[t][k] = the k-th selected
+// expert if its affinity is nonzero, else -1; each nonzero affinity sets bit t % 64 of the
+// token's 64-token chunk mask of its expert, chunk_masks[t / 64][e] (zeroed by the logits
+// kernel; an OR commutes, so the masks are those bw_count_kernel writes).  The workgroups
+// also fill token_position_to_id with -1.  P: values per lane.
+constexpr int kPfTopkTok = 4;
+template <int P>
+__global__ void __launch_bounds__(256) pf_topk_kernel(
     const float* __restrict__ part, const void* __restrict__ bias, int bias_dt, int bias_rnd,
     int logit_rnd, int T, int E, int K, int act, int act_first, int renorm, float renorm_eps,
-    int rnd, const uint8_t* __restrict__ pmask, int n_chunks, float* __restrict__ aff_m,
-    int32_t* __restrict__ sel, int32_t* __restrict__ counts,
-    unsigned long long* __restrict__ chunk_masks, int32_t* __restrict__ tp2id,
-    int64_t n_slots) {
-  static_assert(W == 16 || W == 64, "16 or 64 lanes per token");
-  constexpr int R = 64 / W;    // tokens per pass of a wave
-  constexpr int NP = 4 / R;    // passes: four tokens per wave
-  __shared__ unsigned long long masks[kMaxE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
-  const int j = lane & (W - 1), row = lane / W;
-  for (int64_t i = (int64_t)c * 1024 + tid; i < n_slots; i += (int64_t)n_chunks * 1024)
+    int rnd, const uint8_t* __restrict__ pmask, float* __restrict__ aff_m,
+    int32_t* __restrict__ sel, unsigned long long* __restrict__ chunk_masks,
+    int32_t* __restrict__ tp2id, int64_t n_slots) {
+  const int tid = threadIdx.x, lane = tid & 63, b = blockIdx.x;
+  for (int64_t i = (int64_t)b * 256 + tid; i < n_slots; i += (int64_t)gridDim.x * 256)
     tp2id[i] = -1;
-  for (int i = tid; i < E; i += 1024) masks[i] = 0ull;
+  const int t = b * kPfTopkTok + wave_id();
+  if (t >= T) return;
   const size_t TE = (size_t)T * E;
-  float v[NP][P];
+  float v[P];
 #pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int t = c * kPfTok + 4 * wave + R * p + row;
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    float r = -INFINITY;
+    if (e < E) {
+      const size_t o = (size_t)t * E + e;
+      float sum = part[o];
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const int e = j + W * i;
-      float r = -INFINITY;
-      if (t < T && e < E) {
-        const size_t o = (size_t)t * E + e;
-        float sum = part[o];
-#pragma unroll
-        for (int q = 1; q < kPfParts; ++q) sum += part[q * TE + o];
-        if (bias) sum += round_to(load_as_f32(bias, e, bias_dt), bias_rnd);
-        r = round_to(sum, logit_rnd);
-      }
-      v[p][i] = r;
+      for (int q = 1; q < kPfParts; ++q) sum += part[q * TE + o];
+      if (bias) sum += round_to(load_as_f32(bias, e, bias_dt), bias_rnd);
+      r = round_to(sum, logit_rnd);
     }
+    v[i] = r;
   }
-  __syncthreads();  // masks cleared
+  int sel_idx[8];
+  float out[8];
+  topk_row_wave<P>(v, E, K, act, act_first, renorm, renorm_eps, rnd, sel_idx, out);
+  const float pm = pmask ? (pmask[t] ? 1.0f : 0.0f) : 1.0f;
+  float* mrow = aff_m + (size_t)t * E;
+  unsigned long long* mk = chunk_masks + (size_t)(t / kPfTok) * E;
+  const unsigned long long bit = 1ull << (t % kPfTok);
 #pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    if (c * kPfTok + 4 * wave + R * p >= T) break;  // the pass's first token
-    const int tl = 4 * wave + R * p + row, t = c * kPfTok + tl;
-    int sel_idx[8];
-    float out[8];
-    topk_row_group<W, P>(v[p], E, K, act, act_first, renorm, renorm_eps, rnd, sel_idx, out);
-    if (t < T) {
-      const float pm = pmask ? (pmask[t] ? 1.0f : 0.0f) : 1.0f;
-      float* mrow = aff_m + (size_t)t * E;
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    if (e >= E) break;
+    float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < P; ++i) {
-        const int e = j + W * i;
-        if (e >= E) break;
-        float a = 0.f;
+    for (int k = 0; k < 8; ++k)
+      if (k < K && sel_idx[k] == e) a = out[k];
+    mrow[e] = pmask ? a * pm : a;
+    if (a != 0.0f) atomicOr(mk + e, bit);
+  }
+  if (lane < K) {
+    int si = -1;
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (k < K && sel_idx[k] == e) a = out[k];
-        mrow[e] = pmask ? a * pm : a;
-        if (a != 0.0f) atomicOr(&masks[e], 1ull << tl);
-      }
-      if (j < K) {
-        int si = -1;
+    for (int k = 0; k < 8; ++k)
+      if (k == lane) si = (sel_idx[k] >= 0 && sel_idx[k] < E && out[k] != 0.0f) ? sel_idx[k] : -1;
+    sel[(size_t)t * K + lane] = si;
+  }
+}
+
+// The mapping's placement, one workgroup of 1024 threads per 64-token chunk c.  Every
+// workgroup reads all chunk masks: tot[e] = the expert's tokens and pre[e] = its tokens in
+// chunks before c (integer sums, so the order of the LDS atomics is free), then scans the
+// experts' block counts into the first slot of each run, expert_pos[e] (as bw_scan_body),
+// and writes its chunk's pairs: slot = expert_pos[e] + pre[e] + (the expert's tokens below t
+// in the chunk), the slot bw_scatter_kernel gives them.  Workgroup 0 also writes
+// block_to_expert[n] = #{e < E - 1 : n >= cum[e]} and the schedule of the GEMMs' M-tile
+// groups: M-tile mt lies in block n = 128 mt / B of expert e = block_to_expert[n], whose
+// real slots come first, clamp(tot[e] - (n - first block of e) B, 0, B) of them; the tile
+// holds r = clamp(that - 128 i, 0, 128) (i = its place in the block) and its weight
+// (16-slot subtiles whose first slot is real) is ceil(r / 16): the weight
+// cte_tile_order_kernel reads off token_position_to_id.
+__global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
+    const int32_t* __restrict__ sel, const unsigned long long* __restrict__ chunk_masks, int T,
+    int E, int K, int n_chunks, int B, int N, int G, int32_t* __restrict__ tp2id,
+    int64_t n_slots, int32_t* __restrict__ block_to_expert, int2* __restrict__ order) {
+  static_assert(kOrderThreads == 1024, "one expert per thread in the block scan");
+  extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
+  __shared__ int tot[kMaxE], pre[kMaxE], cum[kMaxE], pos0[kMaxE], wsum[16];
+  __shared__ OrderLds L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
+  for (int e = tid; e < E; e += 1024) tot[e] = pre[e] = 0;
+  __syncthreads();
+  // All masks, eight per thread in flight at a time.
+  const int nm = n_chunks * E;
+  for (int i0 = 0; i0 < nm; i0 += 8 * 1024) {
+    int n[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (k == j)
-            si = (sel_idx[k] >= 0 && sel_idx[k] < E && out[k] != 0.0f) ? sel_idx[k] : -1;
-        sel[(size_t)t * K + j] = si;
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 1024 + tid;
+      n[u] = i < nm ? __popcll(chunk_masks[i]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 1024 + tid;
+      if (n[u]) {
+        const int e = i % E;
+        atomicAdd(&tot[e], n[u]);
+        if (i / E < c) atomicAdd(&pre[e], n[u]);
       }
     }
   }
   __syncthreads();
-  for (int e = tid; e < E; e += 1024) {
-    const unsigned long long m = masks[e];
-    counts[(size_t)e * n_chunks + c] = __popcll(m);
-    chunk_masks[(size_t)c * E + e] = m;
+  // Inclusive scan of the block counts over experts: wave scan, then across waves.
+  const int e = tid;
+  const int nb = e < E ? (tot[e] + B - 1) / B : 0;
+  int v = nb;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(v, off);
+    if (lane >= off) v += o;
   }
-}
-
-// One workgroup: the mapping's scan, then the GEMMs' schedule.  M-tile mt lies in block
-// n = 128 mt / B, of expert e = block_to_expert[n]; that block holds clamp(tot[e] - (n -
-// first block of e) B, 0, B) real slots first, so the tile holds r = clamp(that - 128 i,
-// 0, 128) (i = its place in the block) and its weight (16-slot subtiles whose first slot
-// is real) is ceil(r / 16): the weight cte_tile_order_kernel reads off
-// token_position_to_id.
-__global__ void __launch_bounds__(kOrderThreads) pf_scan_order_kernel(
-    int32_t* __restrict__ counts, int n_chunks, int E, int B, int N, int G,
-    int32_t* __restrict__ expert_pos, int32_t* __restrict__ block_to_expert,
-    int2* __restrict__ order) {
-  static_assert(kOrderThreads == 1024, "bw_scan_body runs on 1024 threads");
-  extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
-  __shared__ int cum[kMaxE], tot[kMaxE], wsum[16];
-  __shared__ OrderLds L;
-  bw_scan_body(counts, n_chunks, E, B, N, expert_pos, block_to_expert, nullptr, nullptr, cum,
-               tot, wsum);
-  const int n_mtiles = N * (B / kPM);
-  int32_t* s_e = reinterpret_cast<int32_t*>(order_dyn);
-  uint8_t* s_w = order_dyn + 4 * (size_t)n_mtiles;
-  const int per = B / kPM;
-  for (int mt = threadIdx.x; mt < n_mtiles; mt += kOrderThreads) {
-    const int n = mt / per, i = mt - n * per;
-    int lo = 0, hi = E - 1;  // block_to_expert[n], from the scan in LDS
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += wsum[w];
+  if (e < E) {
+    cum[e] = v;
+    pos0[e] = (v - nb) * B;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kPfTok * K; idx += 1024) {
+    const int tl = idx / K, t = c * kPfTok + tl;
+    if (t >= T) break;
+    const int x = sel[(size_t)t * K + idx % K];
+    if (x < 0) continue;
+    const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
+    const int64_t pos = (int64_t)pos0[x] + pre[x] +
+                        __popcll(chunk_masks[(size_t)c * E + x] & below);
+    if (pos < n_slots) tp2id[pos] = t;
+  }
+  if (c != 0) return;
+  // Workgroup 0: block_to_expert and the schedule.
+  auto expert_of_block = [&](int n) {  // #{e < E - 1 : n >= cum[e]} (cum non-decreasing)
+    int lo = 0, hi = E - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (cum[mid] <= n) lo = mid + 1;
       else hi = mid;
     }
-    const int e = lo;
-    const int nb = (tot[e] + B - 1) / B;
-    const int first = cum[e] - nb;
-    const int in_block = min(max(tot[e] - (n - first) * B, 0), B);
+    return lo;
+  };
+  for (int n = tid; n < N; n += 1024) block_to_expert[n] = expert_of_block(n);
+  const int n_mtiles = N * (B / kPM), per = B / kPM;
+  int32_t* s_e = reinterpret_cast<int32_t*>(order_dyn);
+  uint8_t* s_w = order_dyn + 4 * (size_t)n_mtiles;
+  for (int mt = tid; mt < n_mtiles; mt += 1024) {
+    const int n = mt / per, i = mt - n * per;
+    const int x = expert_of_block(n);
+    const int nbx = (tot[x] + B - 1) / B;
+    const int first = cum[x] - nbx;
+    const int in_block = min(max(tot[x] - (n - first) * B, 0), B);
     const int r = min(max(in_block - i * kPM, 0), kPM);
     s_w[mt] = (uint8_t)((r + 15) / 16);
-    s_e[mt] = e;
+    s_e[mt] = x;
   }
   __syncthreads();
   order_pass(s_w, s_e, n_mtiles / G, G, order, L);
 }
 
-// The routed pairs of chunk c: slot = expert_pos[e] + (the expert's tokens in earlier
-// chunks) + (its tokens below t in this chunk), as bw_scatter_kernel places them.
-__global__ void __launch_bounds__(256) pf_scatter_kernel(
-    const int32_t* __restrict__ sel, int T, int E, int K, int n_chunks,
-    const int32_t* __restrict__ prefix, const unsigned long long* __restrict__ chunk_masks,
-    const int32_t* __restrict__ expert_pos, int32_t* __restrict__ tp2id, int64_t n_slots) {
-  const int c = blockIdx.x;
-  for (int idx = threadIdx.x; idx < kPfTok * K; idx += 256) {
-    const int tl = idx / K, t = c * kPfTok + tl;
-    if (t >= T) break;
-    const int e = sel[(size_t)t * K + idx % K];
-    if (e < 0) continue;
-    const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
-    const int rank = prefix[(size_t)e * n_chunks + c] +
-                     __popcll(chunk_masks[(size_t)c * E + e] & below);
-    const int64_t pos = (int64_t)expert_pos[e] + rank;
-    if (pos < n_slots) tp2id[pos] = t;
-  }
-}
-
 struct PfWs {
   float *part, *aff_m;
-  int32_t *sel, *counts, *expert_pos, *tp2id, *b2e;
+  int32_t *sel, *tp2id, *b2e;
   unsigned long long* masks;
   int2* order;
   char* cte;
@@ -377,9 +401,7 @@ static size_t pf_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, 
   c.part = cv.take<float>(kPfParts * T * E);
   c.aff_m = cv.take<float>(T * E);
   c.sel = cv.take<int32_t>(T * K);
-  c.counts = cv.take<int32_t>(nch * E);
   c.masks = cv.take<unsigned long long>(nch * E);
-  c.expert_pos = cv.take<int32_t>(E);
   c.tp2id = cv.take<int32_t>(nb * B);
   c.b2e = cv.take<int32_t>(nb);
   c.order = cv.take<int2>(nb * B / kPM);
@@ -391,10 +413,10 @@ static size_t pf_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, 
 
 template <int ETW>
 static void launch_pf_logits(const RouterSpec& r, dim3 g, int T, int H, int E, float* part,
-                             hipStream_t s) {
+                             unsigned long long* masks, hipStream_t s) {
 #define MXMOE_PFL(XF, WF, OP)                                                           \
   hipLaunchKernelGGL((pf_logits_kernel<ETW, XF, WF, OP>), g, dim3(256), 0, s, r.x, r.w, T, H, \
-                     E, part)
+                     E, part, masks)
   const bool xh = r.x_dt == kF16, wh = r.w_dt == kF16;
   if (r.op == kOpF16) {
     if (xh && wh) MXMOE_PFL(true, true, kOpF16);
@@ -481,39 +503,29 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
   mark_event(stage_events, 0, s);
   if (E <= 64)
     launch_pf_logits<1>(r, dim3((unsigned)nch, (unsigned)((E + 63) / 64), kPfParts), (int)T,
-                        (int)H, (int)E, w.part, s);
+                        (int)H, (int)E, w.part, w.masks, s);
   else
     launch_pf_logits<2>(r, dim3((unsigned)nch, (unsigned)((E + 127) / 128), kPfParts), (int)T,
-                        (int)H, (int)E, w.part, s);
+                        (int)H, (int)E, w.part, w.masks, s);
   const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
-#define MXMOE_PFT(W, P)                                                                       \
-  hipLaunchKernelGGL((pf_topk_kernel<W, P>), dim3((unsigned)nch), dim3(1024), 0, s, w.part,   \
-                     r.bias, r.bias_dt, r.bias_rnd, r.logit_rnd, (int)T, (int)E, top_k,        \
-                     router_act, af, rn, renorm_eps, r.act_rnd, padding_mask, nch, w.aff_m,    \
-                     w.sel, w.counts, w.masks, w.tp2id, n_slots)
-  if (E <= 256 && !(af && router_act == MXMOE_ROUTER_SOFTMAX)) {
-    const int p16 = (int)((E + 15) / 16);
-    if (p16 <= 1) MXMOE_PFT(16, 1);
-    else if (p16 <= 2) MXMOE_PFT(16, 2);
-    else if (p16 <= 4) MXMOE_PFT(16, 4);
-    else if (p16 <= 8) MXMOE_PFT(16, 8);
-    else MXMOE_PFT(16, 16);
-  } else {
-    switch (topk_per_lane((int)E)) {
-      case 1: MXMOE_PFT(64, 1); break;
-      case 2: MXMOE_PFT(64, 2); break;
-      case 4: MXMOE_PFT(64, 4); break;
-      case 8: MXMOE_PFT(64, 8); break;
-      default: MXMOE_PFT(64, 16); break;
-    }
+  const dim3 tg((unsigned)((T + kPfTopkTok - 1) / kPfTopkTok));
+#define MXMOE_PFT(P)                                                                          \
+  hipLaunchKernelGGL(pf_topk_kernel<P>, tg, dim3(256), 0, s, w.part, r.bias, r.bias_dt,       \
+                     r.bias_rnd, r.logit_rnd, (int)T, (int)E, top_k, router_act, af, rn,       \
+                     renorm_eps, r.act_rnd, padding_mask, w.aff_m, w.sel, w.masks, w.tp2id,    \
+                     n_slots)
+  switch (topk_per_lane((int)E)) {
+    case 1: MXMOE_PFT(1); break;
+    case 2: MXMOE_PFT(2); break;
+    case 4: MXMOE_PFT(4); break;
+    case 8: MXMOE_PFT(8); break;
+    default: MXMOE_PFT(16); break;
   }
 #undef MXMOE_PFT
   const int G = prefill_group_tiles(block_size);
-  hipLaunchKernelGGL(pf_scan_order_kernel, dim3(1), dim3(kOrderThreads), (size_t)n_mtiles * 5,
-                     s, w.counts, nch, (int)E, (int)block_size, (int)n_blocks, G, w.expert_pos,
-                     w.b2e, w.order);
-  hipLaunchKernelGGL(pf_scatter_kernel, dim3((unsigned)nch), dim3(256), 0, s, w.sel, (int)T,
-                     (int)E, top_k, nch, w.counts, w.masks, w.expert_pos, w.tp2id, n_slots);
+  hipLaunchKernelGGL(pf_place_kernel, dim3((unsigned)nch), dim3(kOrderThreads),
+                     (size_t)n_mtiles * 5, s, w.sel, w.masks, (int)T, (int)E, top_k, nch,
+                     (int)block_size, (int)n_blocks, G, w.tp2id, n_slots, w.b2e, w.order);
   rc = check_launch("moe_prefill front end");
   if (rc) return rc;
   void* cte_ev[4];
