@@ -574,8 +574,9 @@ def time_linear(dev, gen, settle_s, n_w=64, calls=256):
 
 
 def other_configs(dev, gen, settle_s):
-    """The other workloads of the benchmark, each timed once (hip-graph decode, eager
-    prefill), with its binding-roofline fraction: the MXFP4 linear; the GPT-OSS-20B-shaped
+    """The other workloads of the benchmark, each timed once (hip-graph decode over 200
+    steps after the same settling as the headline, eager prefill), with its
+    binding-roofline fraction: the MXFP4 linear; the GPT-OSS-20B-shaped
     layer at decode (1, 4, 16, 64 tokens) and at prefill (4,096 tokens, uniform and
     Zipf(1.2) routing); the 256-expert top-8 layer with Zipf(1.0) routing at decode (128
     tokens) and prefill (8,192 tokens).  Each workload rotates over 8 layers."""
@@ -592,7 +593,7 @@ def other_configs(dev, gen, settle_s):
                 for dT in dts:
                     xs = [torch.randn(dT, H, device=dev, generator=gen).to(torch.bfloat16)
                           for _ in range(8)]
-                    d = time_decode(layers, xs, experts_touched(layers, xs), shape, 40, 3,
+                    d = time_decode(layers, xs, experts_touched(layers, xs), shape, 200, 10,
                                     settle_s, kernel_steps=16)
                     res[f"{tag}_decode_T{dT}"] = {
                         "tokens_per_s": d["tokens_per_s"], "ms_per_step": d["ms_per_step"],
@@ -677,7 +678,7 @@ def main():
 
     others = None
     if not args.no_other_configs and args.workload == "gptoss120b":
-        others = other_configs(dev, gen, min(args.settle, 0.15))
+        others = other_configs(dev, gen, args.settle)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -13,7 +13,9 @@
 //              activation; the fp32 activation is stored as a bf16 (hi, lo) pair
 //   down       the same streaming kernel over (active expert, 4 row groups of H, or 8
 //              when enough experts are active to fill the chip with half as many
-//              waves); two MFMAs (hi, lo) per product, fp32 bias
+//              waves); the fp32 activation as hi + lo: a tile of at most 8 tokens puts
+//              the tokens' hi and lo rows side by side in one MFMA, a larger one takes
+//              two MFMAs (hi, lo) per product; fp32 bias
 //   combine    out[t] = bf16(sum over the token's experts in ascending id of y * w)
 // Items are independent and each writes its own outputs.
 #include <math.h>
@@ -481,6 +483,7 @@ struct TkgArgs {
   const int32_t* tiles;    // (expert, first slot, tokens, 0) per 16-token tile of the routed
                            // batch, and their count
   const int32_t* n_tiles;
+  uint32_t lo_shift;       // down: bytes from h_hi to h_lo
   uint16_t* out_hi;        // gate_up: h (hi, lo)
   uint16_t* out_lo;
   float* y;                // down: [nq, slots, H] (K part q of every slot's output)
@@ -494,10 +497,16 @@ struct TkgArgs {
 // One work item = (active expert, R row groups) of the projection GATE_UP selects:
 // stream the item's packed weights against the expert's tokens, then the epilogue.
 // gate_up items hold whole gate/up pairs (R even).
-template <int R, int NT, bool GATE_UP, int D>
+// PACK (down items of a tile of at most 8 tokens): the MFMA's 16 columns hold the
+// tokens' hi activation rows (columns 0-7) and their lo rows (columns 8-15), so a
+// product takes one MFMA and one activation load per lane instead of two; the epilogue
+// adds column j + 8 to column j.  Without PACK a down item issues the hi and the lo MFMA.
+template <int R, int NT, bool GATE_UP, int D, bool PACK = false>
 __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, int q = 0) {
   static_assert(!GATE_UP || R % 2 == 0, "gate_up items hold gate/up pairs");
-  constexpr bool SPLIT = !GATE_UP;
+  static_assert(!PACK || (!GATE_UP && NT == 1), "packed items are down items of one tile");
+  constexpr bool SPLIT = !GATE_UP && !PACK;
+  constexpr int TT = PACK ? 8 : 16;  // tokens per pass
   const int lane = threadIdx.x & 63;
   const int H = a.H, I = a.I;
   const int K = GATE_UP ? H : I;
@@ -534,14 +543,15 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
   const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
                            : reinterpret_cast<const char*>(a.h_hi);
   const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
-  for (int tb = 0; tb < ne; tb += 16 * NT) {
+  for (int tb = 0; tb < ne; tb += TT * NT) {
     uint32_t row_off[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int li = tb + 16 * t + (lane & 15);
+      const int li = tb + TT * t + (lane & (TT - 1));
       const int lr = li < ne ? li : tb;
       row_off[t] = GATE_UP ? (uint32_t)a.slot_tok[s0 + lr] * (uint32_t)(2 * H)
                            : (uint32_t)(s0 + lr) * (uint32_t)(2 * I);
+      if (PACK && (lane & 8)) row_off[t] += a.lo_shift;  // columns 8-15: the lo rows
     }
     f32x4 acc[R][NT];
 #pragma unroll
@@ -550,6 +560,25 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
       for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     stream_tile<R, NT, SPLIT, D>(g, b1, b2, row_off, acc);
     typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+    if constexpr (PACK) {
+      // y of token j = (hi sums, column j) + (lo sums, column j + 8), then the bias
+      const int li = tb + (lane & 7);
+      const size_t slot = (size_t)(s0 + (li < ne ? li : 0));
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        f32x4 v = acc[r][0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 8);
+        if (r >= g.rv || (lane & 8) || li >= ne) continue;
+        const int n0 = 16 * (rg0 + r) + 4 * (lane >> 4);
+        if (a.bias && q == 0) {  // the first K part carries the bias
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += bf16_bits_to_f32(a.bias[(size_t)e * H + n0 + i]);
+        }
+        *reinterpret_cast<f32x4*>(a.y + q * a.part_stride + slot * H + n0) = v;
+      }
+      continue;
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int li = tb + 16 * t + (lane & 15);
@@ -612,7 +641,8 @@ __host__ __device__ inline int tkg_items_per_expert(int H, int I, bool gate_up, 
 // can have (every expert, or every possible token tile), waves past the batch's units
 // return at once.  The hardware dispatcher hands a freed wave slot the next workgroup, so
 // batches with more units than slots balance over the SIMDs as they stream.  One token
-// tile per item keeps three waves per SIMD (168 registers).
+// tile per item keeps three waves per SIMD (168 registers).  Down items of one tile
+// choose per item: packed hi/lo columns when the tile holds at most 8 tokens.
 template <int R, int NT, bool GATE_UP, int D, int WPB>
 __global__ void __launch_bounds__(64 * WPB)
     __attribute__((amdgpu_waves_per_eu(NT == 1 ? 3 : 1))) tkg_stream_kernel(TkgArgs a) {
@@ -620,6 +650,14 @@ __global__ void __launch_bounds__(64 * WPB)
   const int u = blockIdx.x * WPB + (WPB == 1 ? 0 : wave_id());
   if (u >= (NT == 1 ? *a.n_tiles : *a.n_active) * ipe * a.nq) return;
   const int item = u / a.nq;
+  if constexpr (!GATE_UP && NT == 1) {
+    const int ne =
+        __builtin_amdgcn_readfirstlane(reinterpret_cast<const int4*>(a.tiles)[item / ipe].z);
+    if (ne <= 8) {
+      tkg_item<R, NT, GATE_UP, D, true>(a, item, ipe, u - item * a.nq);
+      return;
+    }
+  }
   tkg_item<R, NT, GATE_UP, D>(a, item, ipe, u - item * a.nq);
 }
 
@@ -705,20 +743,27 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // fewer row-group items than wave slots and is latency-bound (each wave streams one item
 // with one or two chunks in flight).  Such batches split each item's K into parts, each
 // part its own work unit: gate_up in 2 parts when it has under 2,000 items (the raw part
-// sums go through the activation kernel), the down projection of 4-row-group items into
-// parts of about 1,500 units in all (at most 3; the first part adds the bias and the
-// combine adds the parts in order).  Measured on the 20B-shaped layer, us per step: 1 token
-// 47.4 unsplit -> 37.5; against the earlier thresholds (1,000 items; 400 units, at most 8)
-// on one box, 4 tokens 64.6 -> 61.2, 16 tokens 99.3 -> 95.6, 1 and 64 tokens unchanged (the
-// 64-token down items are the wide ones).  More parts lose: each costs a unit
-// start-up and a combine read (8 down parts at 1 token: +7 us), and so does a gate_up
-// split at 2,700 items and more (16 tokens: +0.5 us; 64 tokens: +16 us).
-// Wide down items (8 row groups, one-wave workgroups, 12 per CU: 3,072 wave slots on 256
-// CUs) split in 2 parts while both parts of every item still fit one round of slots, i.e.
-// under 1,400 items (margin for the expected tile count): 20B-shaped layer, 48 tokens
-// (~965 items) 110.2 -> 103.5 us, 64 tokens (~1,058) 115.0 -> 109.5; 3 parts at 64 tokens
-// gain nothing; on the 120B-shaped layer, whose 24 to 64-token batches have 1,610 to
-// 2,770 wide items, 2 parts lose 5 to 9 us.
+// sums go through the activation kernel).  Measured on the 20B-shaped layer, us per step:
+// 1 token 47.4 unsplit -> 37.5.  More parts lose: each costs a unit start-up and a
+// combine read, and so does a gate_up split at 2,700 items and more (16 tokens: +0.5 us;
+// 64 tokens: +16 us).
+// Down, with the packed hi/lo items (one MFMA per product for tiles of at most 8
+// tokens), from a sweep of item shape x K parts at 4-64 tokens on the 20B- and
+// 120B-shaped layers (same box, two alternating runs each):
+//   * batches whose tiles hold 2.5 tokens or more on average, with under 1,400 wide
+//     items (8 row groups, one-wave workgroups, 12 per CU: 3,072 wave slots on 256 CUs):
+//     wide items in 2 K parts, both parts in one round of slots (20B shape, 24 / 32 / 48
+//     / 64 tokens: 95.6 / 97.5 / 101.7 / 108.5 us; 4-row-group items unsplit 96.2 /
+//     98.8 / 107 / 117.3);
+//   * else 4-row-group items (two chunks in flight, one-wave workgroups) while they
+//     stay under 1.7 rounds of wave slots and do not start a nearly empty round (a last
+//     round under 15 % full): 120B shape 16 / 32 / 48 tokens 135.4 / 199.4 / 239.1 us
+//     against 139.8 / 203.7 / 242.0 with wide items; at 24 tokens (~3,090 items, a
+//     second round of a few items) wide items 171.4 against 173.8; at 64 tokens (~5,400
+//     items, 1.76 rounds) wide 263.5 against 264.2.  Under 800 items they take 2 K parts
+//     (20B shape, 4 tokens: 55.6 us against 57.0 unsplit and 57.7 in 3 parts; 120B
+//     shape, 4 tokens: 62.5 with 1 or 2 parts, 63.8 in 3);
+//   * else wide items, whole K.
 // The smallest batches (under 1,300 gate_up items: 1-3 tokens here, and 4 on the 20B
 // shape) take gate_up items of one gate/up pair over all of K, four chunks in flight, in
 // one-wave workgroups, instead of the 2 K parts: as many units and bytes per unit, no
@@ -730,9 +775,12 @@ inline int64_t tkg_max_tiles(int64_t T, int64_t E, int K) {
 // tokens on the 120B shape (~1,380 items) measured 67.0 -> 69.0: hence the threshold.
 constexpr double kTkgGateUpPairItems = 1300.0;
 constexpr double kTkgGateUpSplitItems = 2000.0;
-constexpr double kTkgDownSplitTarget = 1500.0;
-constexpr int kTkgDownMaxParts = 3;
+constexpr double kTkgWaveSlots = 3072.0;        // one-wave workgroups in one round
 constexpr double kTkgWideSplitItems = 1400.0;
+constexpr double kTkgWideTileTokens = 2.5;      // tokens per tile that favour wide items
+constexpr double kTkgNarrowMaxRounds = 1.7;
+constexpr double kTkgNarrowMinLastRound = 0.15;
+constexpr double kTkgNarrowSplitItems = 800.0;
 struct TkgSplit {
   int nq_gu = 1, nq_dn = 1;    // K parts
   int cpq_gu = 1 << 20, cpq_dn = 1 << 20;  // 128-wide chunks per part
@@ -759,16 +807,19 @@ static TkgSplit tkg_split(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
   sp.gu_pairs = gu_items < kTkgGateUpPairItems;
   if (!sp.gu_pairs && gu_items < kTkgGateUpSplitItems)
     tkg_parts((int)((H + 127) / 128), 2, sp.nq_gu, sp.cpq_gu);
+  const int nc_dn = (int)((I + 127) / 128);
   const double wide_items = tiles * (double)((H / 16 + 7) / 8);
-  sp.dn_wide = wide_items >= 900.0;
-  if (sp.dn_wide) {
-    if (wide_items < kTkgWideSplitItems) tkg_parts((int)((I + 127) / 128), 2, sp.nq_dn, sp.cpq_dn);
+  if ((double)(T * K) >= kTkgWideTileTokens * tiles && wide_items < kTkgWideSplitItems) {
+    sp.dn_wide = true;
+    tkg_parts(nc_dn, 2, sp.nq_dn, sp.cpq_dn);
     return sp;
   }
   const double dn_items = tiles * (double)((H / 16 + 3) / 4);
-  const int want = (int)ceil(kTkgDownSplitTarget / (dn_items > 1.0 ? dn_items : 1.0));
-  tkg_parts((int)((I + 127) / 128), want < 1 ? 1 : (want > kTkgDownMaxParts ? kTkgDownMaxParts : want),
-            sp.nq_dn, sp.cpq_dn);
+  const double rounds = dn_items / kTkgWaveSlots;
+  const bool narrow = rounds < kTkgNarrowMaxRounds &&
+                      (rounds < 1.0 || rounds - floor(rounds) >= kTkgNarrowMinLastRound);
+  sp.dn_wide = !narrow;
+  if (narrow && dn_items < kTkgNarrowSplitItems) tkg_parts(nc_dn, 2, sp.nq_dn, sp.cpq_dn);
   return sp;
 }
 
@@ -823,6 +874,12 @@ static int tkg_check(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int 
                 "moe_tkg: H=%lld and I=%lld must be multiples of 32", (long long)H, (long long)I);
   MXMOE_REQUIRE(top_k >= 1 && top_k <= 8, "moe_tkg: top_k=%d out of range [1, 8]", top_k);
   MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_tkg: unknown activation %d", act);
+  // the streaming items address activations by 32-bit byte offsets from h_hi, the lo
+  // rows included (h_hi and h_lo are each [T k, I] bf16, one after the other)
+  MXMOE_REQUIRE((double)T * top_k * (double)I * 4.0 + (double)(H + I) * 4.0 + 4096.0 <
+                    4294967296.0,
+                "moe_tkg: T=%lld x top_k=%d x I=%lld activations exceed 32-bit offsets",
+                (long long)T, top_k, (long long)I);
   MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO,
                 "moe_tkg: unsupported scale mode %d", scale_mode);
   return MXMOE_OK;
@@ -867,6 +924,7 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
   gu.out_lo = w.h_lo;
   dn.h_hi = w.h_hi;
   dn.h_lo = w.h_lo;
+  dn.lo_shift = (uint32_t)((const char*)w.h_lo - (const char*)w.h_hi);
   dn.wq = dn_q;
   dn.ws = dn_s;
   dn.bias = dn_bias;
@@ -911,13 +969,13 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
       hipLaunchKernelGGL(tkg_act_kernel, dim3((unsigned)((I + 1023) / 1024), (unsigned)S),
                          dim3(256), 0, s, gu, (int)E);
     mark_event(ev, 2, s);
-    // down: with enough items (expected active experts E (1 - (1 - k/E)^T) from the batch
-    // size), 8 row groups per item with one chunk in flight, three waves per SIMD, one
-    // wave per workgroup: a 64-token batch's down items then run in one round, spread
-    // over the CUs one wave at a time so that every CU streams about the same share of
-    // the weights (in 2 K parts when both fit that round).  With few items, 4 row groups
-    // and two chunks in flight per wave.  Each item's K in nq_dn parts: the first part adds
-    // the bias, the combine adds the parts in order.
+    // down (the item shape and K parts from tkg_split, on the expected active experts
+    // E (1 - (1 - k/E)^T)): wide items of 8 row groups with one chunk in flight, three
+    // waves per SIMD, one wave per workgroup, so that a 64-token batch's items run in one
+    // round spread over the CUs one wave at a time and every CU streams about the same
+    // share of the weights; or items of 4 row groups with two chunks in flight.  Each
+    // item's K in nq_dn parts: the first part adds the bias, the combine adds the parts
+    // in order.
     dn.part_stride = (size_t)S * (size_t)H;
     dn.nq = sp.nq_dn;
     dn.cpq = sp.cpq_dn;
