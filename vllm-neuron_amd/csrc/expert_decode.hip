@@ -543,6 +543,33 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
   const char* b1 = GATE_UP ? reinterpret_cast<const char*>(a.x)
                            : reinterpret_cast<const char*>(a.h_hi);
   const char* b2 = GATE_UP ? b1 : reinterpret_cast<const char*>(a.h_lo);
+  // The item's biases, loaded before its weights stream (8-byte loads of 4 columns; their
+  // latency then hides behind the stream instead of following it): gate_up [pair][gate,
+  // up], down [row group].  A bias that is not 8-byte aligned is read in the epilogue.
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  constexpr int NB = GATE_UP ? R : R;
+  u16x4 bpre[NB];
+  const bool use_bias = a.bias && (GATE_UP ? a.nq == 1 : q == 0);
+  const bool bvec = use_bias && ((uintptr_t)a.bias & 7u) == 0;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bpre[j] = u16x4{0, 0, 0, 0};
+  if (bvec) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      size_t idx;
+      if constexpr (GATE_UP) {
+        const int pp = (j / 2) * 2 < g.rv ? j / 2 : 0;  // pairs past the item: pair 0
+        idx = (size_t)e * 2 * I + (j & 1 ? I : 0) + 8 * (rg0 + 2 * pp) + 4 * (lane >> 4);
+      } else {
+        const int r = j < g.rv ? j : 0;
+        idx = (size_t)e * H + 16 * (rg0 + r) + 4 * (lane >> 4);
+      }
+      bpre[j] = *reinterpret_cast<const u16x4*>(a.bias + idx);
+    }
+  }
+  auto bias_of = [&](int j, int i, size_t idx) -> float {
+    return bvec ? bf16_bits_to_f32(bpre[j][i]) : bf16_bits_to_f32(a.bias[idx]);
+  };
   for (int tb = 0; tb < ne; tb += TT * NT) {
     uint32_t row_off[NT];
 #pragma unroll
@@ -559,7 +586,6 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     stream_tile<R, NT, SPLIT, D>(g, b1, b2, row_off, acc);
-    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
     if constexpr (PACK) {
       // y of token j = (hi sums, column j) + (lo sums, column j + 8), then the bias
       const int li = tb + (lane & 7);
@@ -571,9 +597,9 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
         for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 8);
         if (r >= g.rv || (lane & 8) || li >= ne) continue;
         const int n0 = 16 * (rg0 + r) + 4 * (lane >> 4);
-        if (a.bias && q == 0) {  // the first K part carries the bias
+        if (use_bias) {  // the first K part carries the bias
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] += bf16_bits_to_f32(a.bias[(size_t)e * H + n0 + i]);
+          for (int i = 0; i < 4; ++i) v[i] += bias_of(r, i, (size_t)e * H + n0 + i);
         }
         *reinterpret_cast<f32x4*>(a.y + q * a.part_stride + slot * H + n0) = v;
       }
@@ -603,9 +629,9 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float gv = acc[2 * pp][t][i], uv = acc[2 * pp + 1][t][i];
-            if (a.bias) {
-              gv += bf16_bits_to_f32(a.bias[(size_t)e * 2 * I + col0 + i]);
-              uv += bf16_bits_to_f32(a.bias[(size_t)e * 2 * I + I + col0 + i]);
+            if (use_bias) {
+              gv += bias_of(2 * pp, i, (size_t)e * 2 * I + col0 + i);
+              uv += bias_of(2 * pp + 1, i, (size_t)e * 2 * I + I + col0 + i);
             }
             gv = clampf_ref(gv, a.p.gate_lo, a.p.gate_hi);
             uv = clampf_ref(uv, a.p.up_lo, a.p.up_hi);
@@ -620,9 +646,9 @@ __device__ __forceinline__ void tkg_item(const TkgArgs& a, int item, int ipe, in
           if (r >= g.rv) continue;
           const int n0 = 16 * (rg0 + r) + 4 * (lane >> 4);
           f32x4 v = acc[r][t];
-          if (a.bias && q == 0) {  // the first K part carries the bias
+          if (use_bias) {  // the first K part carries the bias
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] += bf16_bits_to_f32(a.bias[(size_t)e * H + n0 + i]);
+            for (int i = 0; i < 4; ++i) v[i] += bias_of(r, i, (size_t)e * H + n0 + i);
           }
           *reinterpret_cast<f32x4*>(a.y + q * a.part_stride + slot * H + n0) = v;
         }
