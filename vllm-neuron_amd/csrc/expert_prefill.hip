@@ -836,6 +836,106 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
   }
 }
 
+// The same combine from the tokens' pairs as the fused prefill front end lists them (slot,
+// expert, masked affinity; at most 8, in top-k order): each wave sorts its token's pairs
+// by expert id (scalar registers: the token is the wave's), then sums the rows of y in
+// that order exactly as cte_combine_kernel does.  No inverse and no mapping reads: the
+// rows of y are the only dependent loads.
+// KM: the largest top-k the instance serves (4 or 8); the pair entries and the rows of y are
+// loaded unconditionally (entries past K re-read entry 0, rows past the token's pairs
+// re-read its first row), so that each batch of loads issues together and is waited for
+// once: loads under per-entry conditions were each waited for on their own.
+template <int KM>
+__global__ void __launch_bounds__(kCombineThreads) cte_combine_tok_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ tslot,
+    const int32_t* __restrict__ tsel, const float* __restrict__ tval, int T, int H, int K,
+    int scale_mode, int out_f32, void* __restrict__ out) {
+  static_assert(KM == 4 || KM == 8, "pairs per token");
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kCombineTok + wave_id();
+  if (t >= T) return;
+  // Lane k < KM loads entry k; the values are then taken into scalar registers.
+  const size_t li = (size_t)t * K + (lane < K ? lane : 0);
+  const int le = tsel[li], ls = tslot[li];
+  const float lw = tval[li];
+  int es[KM], ss[KM];
+  float ws[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    const int e = __builtin_amdgcn_readlane(le, k), sl = __builtin_amdgcn_readlane(ls, k);
+    const bool ok = k < K && e >= 0 && sl >= 0;
+    es[k] = ok ? e : 0x7fffffff;  // pairs that are none sort last
+    ss[k] = ok ? sl : 0;
+    ws[k] = scale_mode == MXMOE_SCALE_NO ? 1.0f
+                                         : __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                         __builtin_bit_cast(int, lw), k));
+  }
+  // ascending expert id (ids are distinct): a transposition sort
+#pragma unroll
+  for (int i = 0; i < KM; ++i)
+#pragma unroll
+    for (int j = (i & 1); j + 1 < KM; j += 2)
+      if (es[j] > es[j + 1]) {
+        const int te = es[j], tsl = ss[j];
+        const float tw = ws[j];
+        es[j] = es[j + 1];
+        ss[j] = ss[j + 1];
+        ws[j] = ws[j + 1];
+        es[j + 1] = te;
+        ss[j + 1] = tsl;
+        ws[j + 1] = tw;
+      }
+  int cnt = 0;
+#pragma unroll
+  for (int k = 0; k < KM; ++k) cnt += es[k] != 0x7fffffff ? 1 : 0;
+  // NG column groups of 8 per lane and pass, KM rows each: all NG x KM loads in flight.
+  constexpr int NG = 16 / KM;
+  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+  for (int n = lane * 8; n < H; n += 64 * 8 * NG) {
+    u16x8 b[NG][KM];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int ng = n + 512 * g < H ? n + 512 * g : n;  // a group past H re-reads group 0
+#pragma unroll
+      for (int k = 0; k < KM; ++k)
+        b[g][k] = *reinterpret_cast<const u16x8*>(y + (size_t)ss[k < cnt ? k : 0] * H + ng);
+    }
+    // Every row is an operand here: the compiler would otherwise sink each load into the
+    // condition on its use below and wait for it there, one row at a time.
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if constexpr (KM == 4)
+        asm volatile("" ::"v"(b[g][0]), "v"(b[g][1]), "v"(b[g][2]), "v"(b[g][3]));
+      else
+        asm volatile("" ::"v"(b[g][0]), "v"(b[g][1]), "v"(b[g][2]), "v"(b[g][3]), "v"(b[g][4]),
+                     "v"(b[g][5]), "v"(b[g][6]), "v"(b[g][7]));
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int ng = n + 512 * g;
+      if (ng >= H) break;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        if (k >= cnt) break;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          acc[i] = __fadd_rn(acc[i], __fmul_rn(bf16_bits_to_f32(b[g][k][i]), ws[k]));
+      }
+      if (out_f32) {
+        float* o = static_cast<float*>(out) + (size_t)t * H + ng;
+        *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+      } else {
+        u16x8 r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = f32_to_bf16_bits(acc[i]);
+        *reinterpret_cast<u16x8*>(static_cast<uint16_t*>(out) + (size_t)t * H + ng) = r;
+      }
+    }
+  }
+}
+
 // The affinity of slot p (token tk, expert e) as the reference's pre-scaling modes use it:
 // a bf16 tensor (moe_cte.py:518-520, 556-558 multiply bf16 hidden rows / intermediates by
 // it), so the fp32 value is rounded to bf16.
@@ -1044,6 +1144,11 @@ extern "C" int mxmoe_moe_tkg_bf16(const uint16_t* x, const int32_t* topk_idx,
                 "moe_tkg_bf16: unsupported scale mode %d", scale_mode);
   MXMOE_REQUIRE((uintptr_t)gu_w % 16 == 0 && (uintptr_t)dn_w % 16 == 0,
                 "moe_tkg_bf16: bf16 weights must be 16-byte aligned");
+  // both decode flows address one expert's weights through a buffer resource (32-bit size
+  // and offsets): its gate_up, H x 2I bf16, stays under 4 GiB
+  MXMOE_REQUIRE((double)H * (double)I * 4.0 < 4294967296.0,
+                "moe_tkg_bf16: a bf16 expert's gate_up (H=%lld x 2I=%lld) exceeds 4 GiB",
+                (long long)H, (long long)(2 * I));
   if (tkg_bf16_streams(T, E, top_k))
     return tkg_bf16_stream(x, topk_idx, topk_val, gu_w, dn_w, gu_bias, dn_bias, T, H, I, E, top_k,
                            act, clamps, scale_mode, out, workspace, workspace_bytes,
@@ -1129,7 +1234,7 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
             int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I, int64_t E,
             int act, const float* clamps, int scale_mode, int out_f32, void* out,
             void* workspace, size_t workspace_bytes, void* const* stage_events,
-            const int2* order_pre, hipStream_t s) {
+            const int2* order_pre, hipStream_t s, const CteTokPairs* pairs) {
   const bool bf16w = weight_fmt == MXMOE_WFMT_BF16;
   MXMOE_REQUIRE(x && affinities_masked && gu_q && dn_q && (bf16w || (gu_s && dn_s)) &&
                     token_position_to_id && block_to_expert && out && workspace,
@@ -1143,9 +1248,13 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
   MXMOE_REQUIRE(act >= 0 && act <= 2, "moe_cte: unknown activation %d", act);
   MXMOE_REQUIRE(weight_fmt == MXMOE_WFMT_MXFP4 || weight_fmt == MXMOE_WFMT_MXFP8 || bf16w,
                 "moe_cte: unknown weight format %d", weight_fmt);
-  // bf16 weight rows are read 16 bytes at a time
+  // bf16 weight rows are read 16 bytes at a time, through buffer resources of one expert
+  // (32-bit sizes and offsets)
   MXMOE_REQUIRE(!bf16w || ((uintptr_t)gu_q % 16 == 0 && (uintptr_t)dn_q % 16 == 0),
                 "moe_cte: bf16 weights must be 16-byte aligned");
+  MXMOE_REQUIRE(!bf16w || (double)H * (double)I * 4.0 < 4294967296.0,
+                "moe_cte: a bf16 expert's gate_up (H=%lld x 2I=%lld) exceeds 4 GiB",
+                (long long)H, (long long)(2 * I));
   MXMOE_REQUIRE(scale_mode == MXMOE_SCALE_POST || scale_mode == MXMOE_SCALE_NO ||
                     scale_mode == MXMOE_SCALE_PRE || scale_mode == MXMOE_SCALE_PRE_DELAYED,
                 "moe_cte: unsupported scale mode %d", scale_mode);
@@ -1180,7 +1289,8 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
   a.order = order_pre ? order_pre : w.order;
   a.E = (int)E;
   a.a_by_slot = pre ? 1 : 0;
-  a.inv = w.inv;
+  const bool tok_pairs = pairs && pairs->K <= 8 && !pre && !delayed;
+  a.inv = tok_pairs ? nullptr : w.inv;
   a.p.gate_lo = clamps ? clamps[0] : -INFINITY;
   a.p.gate_hi = clamps ? clamps[1] : INFINITY;
   a.p.up_lo = clamps ? clamps[2] : -INFINITY;
@@ -1235,6 +1345,16 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
                        dim3((unsigned)T, (unsigned)((H + 2047) / 2048)), dim3(256), 0, s, w.y,
                        w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
                        expert_const, (int)H, (int)E, out_f32, out);
+  else if (tok_pairs && pairs->K <= 4)
+    hipLaunchKernelGGL(cte_combine_tok_kernel<4>,
+                       dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
+                       dim3(kCombineThreads), 0, s, w.y, pairs->slot, pairs->sel, pairs->val,
+                       (int)T, (int)H, pairs->K, scale_mode, out_f32, out);
+  else if (tok_pairs)
+    hipLaunchKernelGGL(cte_combine_tok_kernel<8>,
+                       dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
+                       dim3(kCombineThreads), 0, s, w.y, pairs->slot, pairs->sel, pairs->val,
+                       (int)T, (int)H, pairs->K, scale_mode, out_f32, out);
   else
     hipLaunchKernelGGL(cte_combine_kernel<uint16_t>,
                        dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),

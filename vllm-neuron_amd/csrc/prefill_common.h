@@ -222,9 +222,22 @@ void launch_decode_gemm_bf16(bool gate_up, const PrefillArgs& a, const uint16_t*
                              uint16_t* out_lo, float* y32, hipStream_t s);
 int prefill_ntiles_bf16(bool gate_up, int64_t I, int64_t H);
 
+// A token's routed pairs as the fused prefill front end writes them, in top-k order:
+// slot[t K + k] (-1: none), sel[t K + k] the expert (-1: none), val[t K + k] the masked
+// affinity (the value the masked affinities hold for that expert).
+struct CteTokPairs {
+  const int32_t* slot;
+  const int32_t* sel;
+  const float* val;
+  int K;
+};
+
 // The moe_cte flow (expert_prefill.hip): gate_up GEMM, down GEMM, combine over a blockwise
 // mapping.  order_pre: the M-tile groups' schedule already computed (the fused prefill
-// router writes it); null: computed from the mapping first.
+// router writes it); null: computed from the mapping first.  pairs: the tokens' routed
+// pairs (the fused prefill front end writes them; POST_SCALE and NO_SCALE only): the
+// combine reads them instead of the (token, expert) -> slot inverse the gate_up GEMM
+// otherwise writes; null: the inverse.
 int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu_q,
             const uint8_t* gu_s, const uint8_t* dn_q, const uint8_t* dn_s, int weight_fmt,
             const uint16_t* gu_bias, const uint16_t* dn_bias, const uint16_t* expert_const,
@@ -232,6 +245,6 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
             int64_t n_blocks, int64_t block_size, int64_t T, int64_t H, int64_t I, int64_t E,
             int act, const float* clamps, int scale_mode, int out_f32, void* out,
             void* workspace, size_t workspace_bytes, void* const* stage_events,
-            const int2* order_pre, hipStream_t s);
+            const int2* order_pre, hipStream_t s, const CteTokPairs* pairs = nullptr);
 
 }  // namespace mxmoe

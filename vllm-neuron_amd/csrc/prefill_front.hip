@@ -224,7 +224,8 @@ __global__ void __launch_bounds__(256) pf_logits_kernel(const uint16_t* __restri
 // the router kernel forms them (partial sums 0..3 in order, plus the bias rounded to
 // bias_rnd, the sum rounded to logit_rnd), top-k and activation, the masked affinity row
 // aff_m[t] (a * padding_mask, as bw_count_kernel writes it), sel[t][k] = the k-th selected
-// expert if its affinity is nonzero, else -1; each nonzero affinity sets bit t % 64 of the
+// expert if its affinity is nonzero, else -1, and val[t][k] its masked affinity (the value
+// aff_m[t] holds for it: the combine's weight); each nonzero affinity sets bit t % 64 of the
 // token's 64-token chunk mask of its expert, chunk_masks[t / 64][e] (zeroed by the logits
 // kernel; an OR commutes, so the masks are those bw_count_kernel writes).  The workgroups
 // also fill token_position_to_id with -1.  P: values per lane.
@@ -234,8 +235,9 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
     const float* __restrict__ part, const void* __restrict__ bias, int bias_dt, int bias_rnd,
     int logit_rnd, int T, int E, int K, int act, int act_first, int renorm, float renorm_eps,
     int rnd, const uint8_t* __restrict__ pmask, float* __restrict__ aff_m,
-    int32_t* __restrict__ sel, unsigned long long* __restrict__ chunk_masks,
-    int32_t* __restrict__ tp2id, int64_t n_slots) {
+    int32_t* __restrict__ sel, float* __restrict__ val,
+    unsigned long long* __restrict__ chunk_masks, int32_t* __restrict__ tp2id,
+    int64_t n_slots) {
   const int tid = threadIdx.x, lane = tid & 63, b = blockIdx.x;
   for (int64_t i = (int64_t)b * 256 + tid; i < n_slots; i += (int64_t)gridDim.x * 256)
     tp2id[i] = -1;
@@ -277,10 +279,15 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
   }
   if (lane < K) {
     int si = -1;
+    float sv = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (k == lane) si = (sel_idx[k] >= 0 && sel_idx[k] < E && out[k] != 0.0f) ? sel_idx[k] : -1;
+      if (k == lane) {
+        si = (sel_idx[k] >= 0 && sel_idx[k] < E && out[k] != 0.0f) ? sel_idx[k] : -1;
+        sv = out[k];
+      }
     sel[(size_t)t * K + lane] = si;
+    val[(size_t)t * K + lane] = pmask ? sv * pm : sv;
   }
 }
 
@@ -289,7 +296,8 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
 // chunks before c (integer sums, so the order of the LDS atomics is free), then scans the
 // experts' block counts into the first slot of each run, expert_pos[e] (as bw_scan_body),
 // and writes its chunk's pairs: slot = expert_pos[e] + pre[e] + (the expert's tokens below t
-// in the chunk), the slot bw_scatter_kernel gives them.  Workgroup 0 also writes
+// in the chunk), the slot bw_scatter_kernel gives them, and tslot[t][k] = that slot (-1:
+// none), the pair list the combine reads.  Workgroup 0 also writes
 // block_to_expert[n] = #{e < E - 1 : n >= cum[e]} and the schedule of the GEMMs' M-tile
 // groups: M-tile mt lies in block n = 128 mt / B of expert e = block_to_expert[n], whose
 // real slots come first, clamp(tot[e] - (n - first block of e) B, 0, B) of them; the tile
@@ -299,7 +307,8 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
 __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
     const int32_t* __restrict__ sel, const unsigned long long* __restrict__ chunk_masks, int T,
     int E, int K, int n_chunks, int B, int N, int G, int32_t* __restrict__ tp2id,
-    int64_t n_slots, int32_t* __restrict__ block_to_expert, int2* __restrict__ order) {
+    int64_t n_slots, int32_t* __restrict__ tslot, int32_t* __restrict__ block_to_expert,
+    int2* __restrict__ order) {
   static_assert(kOrderThreads == 1024, "one expert per thread in the block scan");
   extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
   __shared__ int tot[kMaxE], pre[kMaxE], cum[kMaxE], pos0[kMaxE], wsum[16];
@@ -348,11 +357,17 @@ __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
     const int tl = idx / K, t = c * kPfTok + tl;
     if (t >= T) break;
     const int x = sel[(size_t)t * K + idx % K];
-    if (x < 0) continue;
-    const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
-    const int64_t pos = (int64_t)pos0[x] + pre[x] +
-                        __popcll(chunk_masks[(size_t)c * E + x] & below);
-    if (pos < n_slots) tp2id[pos] = t;
+    int32_t sl = -1;
+    if (x >= 0) {
+      const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
+      const int64_t pos = (int64_t)pos0[x] + pre[x] +
+                          __popcll(chunk_masks[(size_t)c * E + x] & below);
+      if (pos < n_slots) {
+        tp2id[pos] = t;
+        sl = (int32_t)pos;
+      }
+    }
+    tslot[(size_t)t * K + idx % K] = sl;
   }
   if (c != 0) return;
   // Workgroup 0: block_to_expert and the schedule.
@@ -384,8 +399,8 @@ __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
 }
 
 struct PfWs {
-  float *part, *aff_m;
-  int32_t *sel, *tp2id, *b2e;
+  float *part, *aff_m, *val;
+  int32_t *sel, *tslot, *tp2id, *b2e;
   unsigned long long* masks;
   int2* order;
   char* cte;
@@ -401,6 +416,8 @@ static size_t pf_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, 
   c.part = cv.take<float>(kPfParts * T * E);
   c.aff_m = cv.take<float>(T * E);
   c.sel = cv.take<int32_t>(T * K);
+  c.val = cv.take<float>(T * K);
+  c.tslot = cv.take<int32_t>(T * K);
   c.masks = cv.take<unsigned long long>(nch * E);
   c.tp2id = cv.take<int32_t>(nb * B);
   c.b2e = cv.take<int32_t>(nb);
@@ -512,8 +529,8 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
 #define MXMOE_PFT(P)                                                                          \
   hipLaunchKernelGGL(pf_topk_kernel<P>, tg, dim3(256), 0, s, w.part, r.bias, r.bias_dt,       \
                      r.bias_rnd, r.logit_rnd, (int)T, (int)E, top_k, router_act, af, rn,       \
-                     renorm_eps, r.act_rnd, padding_mask, w.aff_m, w.sel, w.masks, w.tp2id,    \
-                     n_slots)
+                     renorm_eps, r.act_rnd, padding_mask, w.aff_m, w.sel, w.val, w.masks,      \
+                     w.tp2id, n_slots)
   switch (topk_per_lane((int)E)) {
     case 1: MXMOE_PFT(1); break;
     case 2: MXMOE_PFT(2); break;
@@ -525,7 +542,8 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
   const int G = prefill_group_tiles(block_size);
   hipLaunchKernelGGL(pf_place_kernel, dim3((unsigned)nch), dim3(kOrderThreads),
                      (size_t)n_mtiles * 5, s, w.sel, w.masks, (int)T, (int)E, top_k, nch,
-                     (int)block_size, (int)n_blocks, G, w.tp2id, n_slots, w.b2e, w.order);
+                     (int)block_size, (int)n_blocks, G, w.tp2id, n_slots, w.tslot, w.b2e,
+                     w.order);
   rc = check_launch("moe_prefill front end");
   if (rc) return rc;
   void* cte_ev[4];
@@ -534,7 +552,8 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
     for (int i = 0; i < 4; ++i) cte_ev[i] = stage_events[i + 1];
     cev = cte_ev;
   }
+  const CteTokPairs pairs = {w.tslot, w.sel, w.val, top_k};
   return cte_run(x, w.aff_m, gu_q, gu_s, dn_q, dn_s, weight_fmt, gu_bias, dn_bias, nullptr,
                  w.tp2id, w.b2e, n_blocks, block_size, T, H, I, E, act, clamps,
-                 MXMOE_SCALE_POST, out_f32, out, w.cte, w.cte_bytes, cev, w.order, s);
+                 MXMOE_SCALE_POST, out_f32, out, w.cte, w.cte_bytes, cev, w.order, s, &pairs);
 }
