@@ -103,3 +103,22 @@ def test_fused_prefill_workspace_error(dev):
         out.data_ptr(), ws.data_ptr(), ws.numel(), None, _lib.stream_handle(dev))
     assert rc == -3  # MXMOE_E_WORKSPACE
     assert b"workspace" in L.mxmoe_last_error()
+
+
+@pytest.mark.parametrize("E,K", [(8, 1), (16, 3), (32, 5)])
+def test_fused_prefill_top_k_counts(dev, E, K):
+    """Top-k counts other than 2, 4 and 8: the combine reads the first K of its 4 or 8
+    per-token pair entries (the rest re-read entry 0 and are dropped) and sorts them by
+    expert.  Against the operator sequence bit for bit, and against the oracle."""
+    from moe_helpers import PREFILL_FP32_MEAN, check_close, routing_agreement
+    from vllm_neuron_amd import synthetic
+
+    shape = synthetic.MoEShape(f"top{K}", E, K, 256, 512)
+    ref, layer, _ = build(shape, 60 + K, dev, exp=(118, 122))
+    x = synthetic.tokens(60 + K, 513, shape.H)
+    print(f"fused prefill top-{K} of {E}", flush=True)
+    _equal(layer, x.to(dev))
+    aff, ties = routing_agreement(layer, ref, x, dev)
+    got = layer.prefill(x.to(dev), output_dtype=torch.float32).cpu()
+    want = ref.prefill_routed(x, aff)
+    check_close(got, want, ties, f"fused prefill top-{K}", mean_bound=PREFILL_FP32_MEAN)
