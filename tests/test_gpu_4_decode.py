@@ -263,3 +263,31 @@ def test_decode_gptoss120b_t64(dev):
     got, aff, ties = decode_checked(layer, ref, x, dev)
     want = ref.decode_routed(x, aff)
     check_close(got, want, ties, "decode 120b T=64", ulp=BF16_OUT)
+
+
+@pytest.mark.parametrize("T", [4, 64])
+def test_decode_unaligned_biases(dev, gptoss20, T):
+    """Biases that are not 8-byte aligned (a view 2 bytes into its storage) take the
+    epilogue's element loads instead of the 8-byte loads issued before the weights
+    stream; the arithmetic is the same, so the outputs are bit-identical."""
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.layer import MXFP4MoE
+
+    ref, layer, _ = gptoss20
+    w = layer.w
+    x = synthetic.tokens(71, T, ref.H).to(dev)
+    want = layer.decode(x)
+
+    def shifted(b):
+        buf = torch.empty(b.numel() + 1, dtype=b.dtype, device=b.device)
+        v = buf[1:].view(b.shape)
+        v.copy_(b)
+        assert v.data_ptr() % 8 == 2
+        return v
+
+    import dataclasses
+    w2 = dataclasses.replace(w, gu_bias=shifted(w.gu_bias), dn_bias=shifted(w.dn_bias))
+    lay2 = MXFP4MoE(w2, layer.router_w, layer.router_b, layer.top_k, layer.limit)
+    got = lay2.decode(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
