@@ -807,12 +807,14 @@ constexpr double kTkgWideTileTokens = 2.5;      // tokens per tile that favour w
 constexpr double kTkgNarrowMaxRounds = 1.7;
 constexpr double kTkgNarrowMinLastRound = 0.15;
 constexpr double kTkgNarrowSplitItems = 800.0;
+constexpr double kTkgGuWideMinRounds = 1.2, kTkgGuWideMaxRounds = 1.7;
 struct TkgSplit {
   int nq_gu = 1, nq_dn = 1;    // K parts
   int cpq_gu = 1 << 20, cpq_dn = 1 << 20;  // 128-wide chunks per part
   bool one_tile = true;
   bool gu_pairs = false;       // gate_up items of one gate/up pair, all of K
   bool dn_wide = false;        // down items of 8 row groups, one chunk in flight
+  bool gu_wide = false;        // gate_up items of 8 row groups (4 pairs), one chunk in flight
 };
 
 // q K parts of nc chunks: cpq = ceil(nc / q) chunks each, and the part count recomputed
@@ -831,7 +833,19 @@ static TkgSplit tkg_split(int64_t T, int64_t H, int64_t I, int64_t E, int K) {
   const double tiles = active + ((double)(T * K) - active) / 16.0;  // 16-token tiles
   const double gu_items = tiles * (double)((2 * I / 16 + 3) / 4);
   sp.gu_pairs = gu_items < kTkgGateUpPairItems;
-  if (!sp.gu_pairs && gu_items < kTkgGateUpSplitItems)
+  // gate_up items of 4 pairs, one chunk in flight, one-wave workgroups, when items of 2
+  // pairs would make between 1.2 and 1.7 rounds of wave slots and the tiles hold 2.5
+  // tokens or more on average: the wide items then run in one round and read each
+  // activation row once per 8 row groups instead of 4.  Same box, alternating runs, us per
+  // step: 20B-shaped layer 48 / 56 / 64 tokens (4.6-5.6 tokens per tile) 100.4 / 103.6 /
+  // 107.1 -> 100.1 / 102.1 / 104.2; with about one token per tile they lose (120B shape 12
+  // and 16 tokens +2.4 and +7.9, 256-expert layer 8 tokens +1.7), as they do outside that
+  // range of rounds (20B shape 24 and 32 tokens, just over one round, +1.1 to +1.5; 120B
+  // shape 24 to 64 tokens, 2 to 3.3 rounds, +2.5 to +11).
+  const double gu_rounds = gu_items / kTkgWaveSlots;
+  sp.gu_wide = !sp.gu_pairs && gu_rounds >= kTkgGuWideMinRounds &&
+               gu_rounds < kTkgGuWideMaxRounds && (double)(T * K) >= kTkgWideTileTokens * tiles;
+  if (!sp.gu_pairs && !sp.gu_wide && gu_items < kTkgGateUpSplitItems)
     tkg_parts((int)((H + 127) / 128), 2, sp.nq_gu, sp.cpq_gu);
   const int nc_dn = (int)((I + 127) / 128);
   const double wide_items = tiles * (double)((H / 16 + 7) / 8);
@@ -984,6 +998,9 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
     if (sp.gu_pairs)
       hipLaunchKernelGGL((tkg_stream_kernel<2, 1, true, 4, 1>),
                          dim3(grid(true, 2, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
+    else if (sp.gu_wide)
+      hipLaunchKernelGGL((tkg_stream_kernel<8, 1, true, 1, 1>),
+                         dim3(grid(true, 8, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
     else if (sp.nq_gu == 1 && T <= 16)
       hipLaunchKernelGGL((tkg_stream_kernel<4, 1, true, 2, 1>),
                          dim3(grid(true, 4, 1, n_tile_max).x), dim3(64), kLds12x1, s, gu);
