@@ -729,7 +729,12 @@ __global__ void __launch_bounds__(256) tkg_act_kernel(TkgArgs a, int E) {
 }
 
 // out[t, n] = bf16(sum_k y[slot(t, k), n] * w(t, k)), k in ascending expert order, each
-// y the sum of its nq K parts in order.
+// y the sum of its nq K parts in order.  KM (4 or 8) >= top-k: the token's slots and
+// weights are loaded first (entries past K re-read entry 0), then the rows of K part 0 of
+// every entry (an absent slot reads row 0), all in flight before the first is used; with
+// a condition per entry the compiler waited for each load on its own.  KM = 0: any top-k,
+// one entry at a time.
+template <int KM>
 __global__ void __launch_bounds__(256) tkg_combine_kernel(const float* __restrict__ y,
                                                           const int32_t* __restrict__ tok_slot,
                                                           const float* __restrict__ tok_w, int H,
@@ -738,24 +743,78 @@ __global__ void __launch_bounds__(256) tkg_combine_kernel(const float* __restric
   const int t = blockIdx.y;
   const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= H) return;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < K; ++k) {
-    const int s = tok_slot[(size_t)t * K + k];
-    if (s < 0) continue;
-    const float w = tok_w[(size_t)t * K + k];
-    f32x4 v = *reinterpret_cast<const f32x4*>(y + (size_t)s * H + n);
-    for (int q = 1; q < nq; ++q) {
-      const f32x4 vq = *reinterpret_cast<const f32x4*>(y + q * part_stride + (size_t)s * H + n);
+  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+  if constexpr (KM == 0) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < K; ++k) {
+      const int s = tok_slot[(size_t)t * K + k];
+      if (s < 0) continue;
+      const float w = tok_w[(size_t)t * K + k];
+      f32x4 v = *reinterpret_cast<const f32x4*>(y + (size_t)s * H + n);
+      for (int q = 1; q < nq; ++q) {
+        const f32x4 vq = *reinterpret_cast<const f32x4*>(y + q * part_stride + (size_t)s * H + n);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], vq[i]);
+        for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], vq[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], w));
+    }
+    *reinterpret_cast<u16x4*>(out + (size_t)t * H + n) =
+        u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
+              f32_to_bf16_bits(acc[3])};
+    return;
+  }
+  constexpr int KA = KM > 0 ? KM : 1;
+  int sl[KA];
+  float wt[KA];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    const size_t i = (size_t)t * K + (k < K ? k : 0);
+    sl[k] = tok_slot[i];
+    wt[k] = tok_w[i];
+  }
+  f32x4 v[KA];
+#pragma unroll
+  for (int k = 0; k < KM; ++k)
+    v[k] = *reinterpret_cast<const f32x4*>(y + (size_t)(sl[k] >= 0 ? sl[k] : 0) * H + n);
+  if constexpr (KM == 4)
+    asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
+  else
+    asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]),
+                 "v"(v[6]), "v"(v[7]));
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    if (k >= K || sl[k] < 0) continue;
+    f32x4 vk = v[k];
+    for (int q = 1; q < nq; ++q) {
+      const f32x4 vq =
+          *reinterpret_cast<const f32x4*>(y + q * part_stride + (size_t)sl[k] * H + n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vk[i] = __fadd_rn(vk[i], vq[i]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], w));
+    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(vk[i], wt[k]));
   }
-  typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
   *reinterpret_cast<u16x4*>(out + (size_t)t * H + n) =
       u16x4{f32_to_bf16_bits(acc[0]), f32_to_bf16_bits(acc[1]), f32_to_bf16_bits(acc[2]),
             f32_to_bf16_bits(acc[3])};
+}
+
+// The combine for top-k entries per token.
+static void launch_tkg_combine(const float* y, const int32_t* tok_slot, const float* tok_w,
+                               int64_t T, int64_t H, int K, int nq, size_t part_stride,
+                               uint16_t* out, hipStream_t s) {
+  const dim3 g((unsigned)((H / 4 + 255) / 256), (unsigned)T);
+  if (K <= 4)
+    hipLaunchKernelGGL(tkg_combine_kernel<4>, g, dim3(256), 0, s, y, tok_slot, tok_w, (int)H, K,
+                       nq, part_stride, out);
+  else if (K <= 8)
+    hipLaunchKernelGGL(tkg_combine_kernel<8>, g, dim3(256), 0, s, y, tok_slot, tok_w, (int)H, K,
+                       nq, part_stride, out);
+  else
+    hipLaunchKernelGGL(tkg_combine_kernel<0>, g, dim3(256), 0, s, y, tok_slot, tok_w, (int)H, K,
+                       nq, part_stride, out);
 }
 
 // Token tiles of the routed batch: sum over touched experts of ceil(n_e / 16) with
@@ -1044,9 +1103,7 @@ static int tkg_pipeline(const uint16_t* x, const int32_t* topk_idx, const float*
                        s, dn);
   }
   mark_event(ev, 3, s);
-  hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
-                     dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, dn.nq,
-                     dn.part_stride, out);
+  launch_tkg_combine(w.y, w.tok_slot, w.tok_w, T, H, top_k, dn.nq, dn.part_stride, out, s);
   mark_event(ev, 4, s);
   return check_launch("moe_tkg");
 }
@@ -1324,9 +1381,7 @@ int tkg_bf16_stream(const uint16_t* x, const int32_t* topk_idx, const float* top
   dn.part_stride = (size_t)S * (size_t)H;
   hipLaunchKernelGGL(tkgb_stream_kernel<false>, blocks(H, pl.nq_dn), dim3(64 * kBdWaves), 0, s,
                      dn, w.y, dn.part_stride);
-  hipLaunchKernelGGL(tkg_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T),
-                     dim3(256), 0, s, w.y, w.tok_slot, w.tok_w, (int)H, top_k, pl.nq_dn,
-                     dn.part_stride, out);
+  launch_tkg_combine(w.y, w.tok_slot, w.tok_w, T, H, top_k, pl.nq_dn, dn.part_stride, out, s);
   return check_launch("moe_tkg_bf16");
 }
 
