@@ -86,11 +86,24 @@ __device__ __forceinline__ float round_to(float f, int dt) {
   return f;
 }
 
-// Element i of an array of element type dt, as fp32 (exact).
+// Element i of an array of element type dt, as fp32 (exact).  Branch-free: two 16-bit
+// loads that are always issued (an fp32 element's halves, or the 16-bit element twice),
+// so that several calls' loads issue together instead of one basic block per load.
 __device__ __forceinline__ float load_as_f32(const void* p, size_t i, int dt) {
-  if (dt == kF32) return static_cast<const float*>(p)[i];
-  const uint16_t b = static_cast<const uint16_t*>(p)[i];
-  return dt == kF16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+  const uint16_t* h = static_cast<const uint16_t*>(p);
+  const bool f32 = dt == kF32;
+  const uint16_t b0 = h[f32 ? 2 * i : i], b1 = h[f32 ? 2 * i + 1 : i];
+  const float v16 = dt == kF16 ? f16_bits_to_f32(b0) : bf16_bits_to_f32(b0);
+  return f32 ? __uint_as_float((uint32_t)b0 | ((uint32_t)b1 << 16)) : v16;
+}
+
+// Element i of an optional array p (null: 0.0f) as fp32.  Its loads are always issued (from
+// `fallback`, any array of at least i + 1 floats, when p is null) and the value is masked
+// by a bit-and, so that no branch puts the loads in a block of their own.
+__device__ __forceinline__ float load_opt_f32(const void* p, size_t i, int dt,
+                                              const void* fallback) {
+  const float v = load_as_f32(p ? p : fallback, i, p ? dt : kF32);
+  return __uint_as_float(__float_as_uint(v) & (p ? 0xffffffffu : 0u));
 }
 
 // Eight 16-bit values (a 16-byte load) in one type, as eight of another.

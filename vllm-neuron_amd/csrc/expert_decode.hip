@@ -54,16 +54,26 @@ __device__ __forceinline__ void tkg_route_block(
     vals[k] = 0.f;
   }
   if (tid < T) {
+    // every entry loaded first (entries past K re-read entry 0), so that the loads issue
+    // together instead of one round trip per entry
+    int ei[8];
+    float vi[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const size_t i = (size_t)tid * K + (k < K ? k : 0);
+      ei[k] = topk_idx[i];
+      vi[k] = topk_val[i];
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (k >= K) break;
-      int e = topk_idx[(size_t)tid * K + k];
+      int e = ei[k];
       if (e < 0 || e >= E) e = -1;
       // A repeated expert id counts once (its last value, as a scatter would keep).
       for (int j = 0; j < k; ++j)
         if (ids[j] == e) ids[j] = -1;
       ids[k] = e;
-      vals[k] = topk_val[(size_t)tid * K + k];
+      vals[k] = vi[k];
       if (e >= 0) atomicOr(&masks[wave][e], 1ull << lane);
     }
   }
@@ -233,7 +243,7 @@ __global__ void __launch_bounds__(1024) front_route_kernel(
   // so the partial sums and the bias arrive in one round trip.
   float bval[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) bval[i] = bias ? load_as_f32(bias, min(j + 16 * i, E - 1), bias_dt) : 0.f;
+  for (int i = 0; i < PER; ++i) bval[i] = load_opt_f32(bias, min(j + 16 * i, E - 1), bias_dt, part);
   for (int t = row; t < T; t += 64) {
     float pv[kFrontSlices][PER];
 #pragma unroll
@@ -288,7 +298,7 @@ __global__ void __launch_bounds__(256) front_topk_kernel(
   float bval[PER];
   float pv[kFrontSlices][PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) bval[i] = bias ? load_as_f32(bias, min(j + 16 * i, E - 1), bias_dt) : 0.f;
+  for (int i = 0; i < PER; ++i) bval[i] = load_opt_f32(bias, min(j + 16 * i, E - 1), bias_dt, part);
 #pragma unroll
   for (int sl = 0; sl < kFrontSlices; ++sl)
 #pragma unroll

@@ -245,16 +245,25 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
   if (t >= T) return;
   const size_t TE = (size_t)T * E;
   float v[P];
+  // every load issued first (lanes past E read expert E - 1 and are dropped), then the sums
+  float pv[P][kPfParts], bv[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int ec = min(lane + 64 * i, E - 1);
+    const size_t o = (size_t)t * E + ec;
+#pragma unroll
+    for (int q = 0; q < kPfParts; ++q) pv[i][q] = part[q * TE + o];
+    bv[i] = load_opt_f32(bias, ec, bias_dt, part);
+  }
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     const int e = lane + 64 * i;
     float r = -INFINITY;
     if (e < E) {
-      const size_t o = (size_t)t * E + e;
-      float sum = part[o];
+      float sum = pv[i][0];
 #pragma unroll
-      for (int q = 1; q < kPfParts; ++q) sum += part[q * TE + o];
-      if (bias) sum += round_to(load_as_f32(bias, e, bias_dt), bias_rnd);
+      for (int q = 1; q < kPfParts; ++q) sum += pv[i][q];
+      if (bias) sum += round_to(bv[i], bias_rnd);
       r = round_to(sum, logit_rnd);
     }
     v[i] = r;

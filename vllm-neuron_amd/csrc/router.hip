@@ -46,7 +46,7 @@ __global__ void __launch_bounds__(64 * NW) router_logits_kernel(
       const int ex = e0 + 16 * e + 4 * q + i;
       if (ex >= E) continue;
       float v = s[i];
-      if (bias) v += round_to(load_as_f32(bias, ex, bias_dt), bias_rnd);
+      if (bias) v += round_to(load_opt_f32(bias, ex, bias_dt, w), bias_rnd);
       logits[(size_t)tok * E + ex] = round_to(v, logit_rnd);
     }
   }
