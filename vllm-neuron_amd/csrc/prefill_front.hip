@@ -300,47 +300,59 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
   }
 }
 
-// The mapping's placement, one workgroup of 1024 threads per 64-token chunk c.  Every
-// workgroup reads all chunk masks: tot[e] = the expert's tokens and pre[e] = its tokens in
-// chunks before c (integer sums, so the order of the LDS atomics is free), then scans the
-// experts' block counts into the first slot of each run, expert_pos[e] (as bw_scan_body),
-// and writes its chunk's pairs: slot = expert_pos[e] + pre[e] + (the expert's tokens below t
-// in the chunk), the slot bw_scatter_kernel gives them, and tslot[t][k] = that slot (-1:
-// none), the pair list the combine reads.  Workgroup 0 also writes
-// block_to_expert[n] = #{e < E - 1 : n >= cum[e]} and the schedule of the GEMMs' M-tile
-// groups: M-tile mt lies in block n = 128 mt / B of expert e = block_to_expert[n], whose
-// real slots come first, clamp(tot[e] - (n - first block of e) B, 0, B) of them; the tile
-// holds r = clamp(that - 128 i, 0, 128) (i = its place in the block) and its weight
-// (16-slot subtiles whose first slot is real) is ceil(r / 16): the weight
-// cte_tile_order_kernel reads off token_position_to_id.
+// The mapping's placement, one workgroup of 1024 threads per 64-token chunk c, and one
+// more (c = n_chunks) for the schedule.  Every workgroup reads all chunk masks: tot[e] =
+// the expert's tokens (integer sums, so the order of the LDS atomics is free), then scans
+// the experts' block counts into the first slot of each run, expert_pos[e] (as
+// bw_scan_body).  A chunk's workgroup also sums pre[e] = the expert's tokens in chunks
+// before c, keeps its own chunk's masks in LDS and writes its chunk's pairs: slot =
+// expert_pos[e] + pre[e] + (the expert's tokens below t in the chunk), the slot
+// bw_scatter_kernel gives them, and tslot[t][k] = that slot (-1: none), the pair list the
+// combine reads; the chunk's selections are loaded with the masks, so no global load
+// waits behind the scan.  The schedule's workgroup writes block_to_expert[n] = #{e < E - 1
+// : n >= cum[e]} and the schedule of the GEMMs' M-tile groups: M-tile mt lies in block
+// n = 128 mt / B of expert e = block_to_expert[n], whose real slots come first,
+// clamp(tot[e] - (n - first block of e) B, 0, B) of them; the tile holds r = clamp(that -
+// 128 i, 0, 128) (i = its place in the block) and its weight (16-slot subtiles whose first
+// slot is real) is ceil(r / 16): the weight cte_tile_order_kernel reads off
+// token_position_to_id.  Dynamic LDS: max(5 B per M-tile, 8 B per expert).
 __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
     const int32_t* __restrict__ sel, const unsigned long long* __restrict__ chunk_masks, int T,
     int E, int K, int n_chunks, int B, int N, int G, int32_t* __restrict__ tp2id,
     int64_t n_slots, int32_t* __restrict__ tslot, int32_t* __restrict__ block_to_expert,
     int2* __restrict__ order) {
   static_assert(kOrderThreads == 1024, "one expert per thread in the block scan");
+  static_assert(kPfTok * 8 <= kOrderThreads, "one pair of the chunk per thread");
   extern __shared__ __attribute__((aligned(16))) uint8_t order_dyn[];
   __shared__ int tot[kMaxE], pre[kMaxE], cum[kMaxE], pos0[kMaxE], wsum[16];
   __shared__ OrderLds L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
+  const bool place = c < n_chunks;
+  unsigned long long* own = reinterpret_cast<unsigned long long*>(order_dyn);
+  // this thread's pair of the chunk (token c * 64 + tid / K, selection tid % K)
+  const int tl = tid / K, tp = c * kPfTok + tl;
+  const bool has_pair = place && tid < kPfTok * K && tp < T;
+  const int xs = place ? sel[has_pair ? (size_t)tp * K + tid % K : 0] : -1;
   for (int e = tid; e < E; e += 1024) tot[e] = pre[e] = 0;
   __syncthreads();
   // All masks, eight per thread in flight at a time.
   const int nm = n_chunks * E;
   for (int i0 = 0; i0 < nm; i0 += 8 * 1024) {
-    int n[8];
+    unsigned long long m[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int i = i0 + u * 1024 + tid;
-      n[u] = i < nm ? __popcll(chunk_masks[i]) : 0;
+      m[u] = i < nm ? chunk_masks[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int i = i0 + u * 1024 + tid;
-      if (n[u]) {
+      const int n = __popcll(m[u]);
+      if (place && i / E == c) own[i % E] = m[u];
+      if (n) {
         const int e = i % E;
-        atomicAdd(&tot[e], n[u]);
-        if (i / E < c) atomicAdd(&pre[e], n[u]);
+        atomicAdd(&tot[e], n);
+        if (i / E < c) atomicAdd(&pre[e], n);
       }
     }
   }
@@ -362,24 +374,22 @@ __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
     pos0[e] = (v - nb) * B;
   }
   __syncthreads();
-  for (int idx = tid; idx < kPfTok * K; idx += 1024) {
-    const int tl = idx / K, t = c * kPfTok + tl;
-    if (t >= T) break;
-    const int x = sel[(size_t)t * K + idx % K];
-    int32_t sl = -1;
-    if (x >= 0) {
-      const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
-      const int64_t pos = (int64_t)pos0[x] + pre[x] +
-                          __popcll(chunk_masks[(size_t)c * E + x] & below);
-      if (pos < n_slots) {
-        tp2id[pos] = t;
-        sl = (int32_t)pos;
+  if (place) {
+    if (has_pair) {
+      int32_t sl = -1;
+      if (xs >= 0) {
+        const unsigned long long below = (tl == 0) ? 0ull : (~0ull >> (64 - tl));
+        const int64_t pos = (int64_t)pos0[xs] + pre[xs] + __popcll(own[xs] & below);
+        if (pos < n_slots) {
+          tp2id[pos] = tp;
+          sl = (int32_t)pos;
+        }
       }
+      tslot[(size_t)tp * K + tid % K] = sl;
     }
-    tslot[(size_t)t * K + idx % K] = sl;
+    return;
   }
-  if (c != 0) return;
-  // Workgroup 0: block_to_expert and the schedule.
+  // The schedule's workgroup: block_to_expert and the schedule.
   auto expert_of_block = [&](int n) {  // #{e < E - 1 : n >= cum[e]} (cum non-decreasing)
     int lo = 0, hi = E - 1;
     while (lo < hi) {
@@ -549,8 +559,8 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
   }
 #undef MXMOE_PFT
   const int G = prefill_group_tiles(block_size);
-  hipLaunchKernelGGL(pf_place_kernel, dim3((unsigned)nch), dim3(kOrderThreads),
-                     (size_t)n_mtiles * 5, s, w.sel, w.masks, (int)T, (int)E, top_k, nch,
+  const size_t place_lds = std::max((size_t)n_mtiles * 5, (size_t)E * 8);
+  hipLaunchKernelGGL(pf_place_kernel, dim3((unsigned)nch + 1), dim3(kOrderThreads), place_lds, s, w.sel, w.masks, (int)T, (int)E, top_k, nch,
                      (int)block_size, (int)n_blocks, G, w.tp2id, n_slots, w.tslot, w.b2e,
                      w.order);
   rc = check_launch("moe_prefill front end");
