@@ -92,23 +92,17 @@ def _pad_cols(x):
     return out
 
 
-@pytest.mark.parametrize("T", [8, 64])
-def test_model_mxfp4_decode_call(dev, layer20, T):
-    """_run_moe_block_tkg's NF.moe_block_tkg call (model_mxfp4.py:1183-1214) verbatim."""
-    from vllm_neuron_amd import functional as NF
-    from vllm_neuron_amd import synthetic
+def _block_tkg_kwargs(p, hidden_states, H, dev):
+    """The keyword arguments of _run_moe_block_tkg's NF.moe_block_tkg call
+    (model_mxfp4.py:1183-1214) on the parameters p."""
     from vllm_neuron_amd.enums import ActFnType, ExpertAffinityScaleMode, RouterActFnType
 
-    lt, ref, p = layer20
-    H = ref.H
-    x = synthetic.tokens(63, T, H)
-    hidden_states = _pad_cols(x).to(dev)
     limit, K, E = 7.0, 4, p.E
     I_TP = p.gate_up_proj_weight.shape[-1]
     n_blk = math.ceil(I_TP / 512.0)
     blk = I_TP // n_blk
     rank_id = torch.tensor([[0]], dtype=torch.int32, device=dev)
-    kw = dict(
+    return dict(
         inp=hidden_states.unsqueeze(0),
         gamma=p.ln_weight.unsqueeze(0).to(torch.float32),
         router_weights=p.router_weight.T,
@@ -135,6 +129,20 @@ def test_model_mxfp4_decode_call(dev, layer20, T):
         is_all_expert=True,
         skip_router_logits=True,
     )
+
+
+@pytest.mark.parametrize("T", [8, 64])
+def test_model_mxfp4_decode_call(dev, layer20, T):
+    """_run_moe_block_tkg's NF.moe_block_tkg call (model_mxfp4.py:1183-1214) verbatim."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+
+    lt, ref, p = layer20
+    H = ref.H
+    K, E = 4, p.E
+    x = synthetic.tokens(63, T, H)
+    hidden_states = _pad_cols(x).to(dev)
+    kw = _block_tkg_kwargs(p, hidden_states, H, dev)
     out = NF.moe_block_tkg(**kw)
     assert out.shape == (T, H_PAD) and out.dtype == torch.bfloat16
     kw["skip_router_logits"] = False
@@ -155,6 +163,44 @@ def test_model_mxfp4_decode_call(dev, layer20, T):
     want = ref.decode_routed(xn_g[:, :H], aff)
     ties = torch.tensor([near_tie(logits_r[t], K) for t in range(T)])
     check_close(out[:, :H], want, ties, f"model_mxfp4 decode call T={T}")
+
+
+def test_model_mxfp4_in_place_experts(dev, layer20):
+    """With in-place conversion on, the model's Trainium-layout parameters are rewritten
+    into packed bytes in their own memory on the first call (no converted copy is kept),
+    and the decode call gives the copy path's output bit for bit, on the first call and
+    on later ones."""
+    import types
+
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.functional.moe import _cache
+    from vllm_neuron_amd.neuron_layout import packed_in_place, set_convert_in_place
+
+    lt, ref, p = layer20
+    H = ref.H
+    x = synthetic.tokens(64, 16, H)
+    hidden_states = _pad_cols(x).to(dev)
+    want = NF.moe_block_tkg(**_block_tkg_kwargs(p, hidden_states, H, dev))
+    q = types.SimpleNamespace(**vars(p))
+    for n in ("gate_up_proj_weight", "gate_up_proj_scale", "down_proj_weight",
+              "down_proj_scale"):
+        setattr(q, n, getattr(p, n).clone())
+    ptr = q.gate_up_proj_weight.data_ptr()
+    prev = set_convert_in_place(True)
+    try:
+        n0 = _cache.entries()
+        got = NF.moe_block_tkg(**_block_tkg_kwargs(q, hidden_states, H, dev))
+        assert packed_in_place(q.gate_up_proj_weight, q.gate_up_proj_scale,
+                               q.down_proj_weight, q.down_proj_scale) is not None
+        assert q.gate_up_proj_weight.data_ptr() == ptr
+        assert torch.equal(got, want)
+        got2 = NF.moe_block_tkg(**_block_tkg_kwargs(q, hidden_states, H, dev))
+        assert torch.equal(got2, want)
+        # only the two bias conversions were cached, no expert copy
+        assert _cache.entries() <= n0 + 2
+    finally:
+        set_convert_in_place(prev)
 
 
 def test_model_mxfp4_prefill_chain(dev, layer20):

@@ -119,3 +119,90 @@ def test_converter_rejects_bad_inputs():
         experts_from_neuron_layout(gub, gus, dnb, dns, 1024, I)
     with pytest.raises(TypeError):
         experts_from_neuron_layout(gub.view(torch.uint8), gus, dnb, dns, H, I)
+
+
+def _neuron_tensors(E, H, I, Hp, Ip, seed):
+    g = torch.Generator().manual_seed(seed)
+    gub = torch.randint(0, 256, (E, 2 * I, H // 32, 16), generator=g, dtype=torch.uint8)
+    gus = torch.randint(0, 256, (E, 2 * I, H // 32), generator=g, dtype=torch.uint8)
+    dnb = torch.randint(0, 256, (E, H, I // 32, 16), generator=g, dtype=torch.uint8)
+    dns = torch.randint(0, 256, (E, H, I // 32), generator=g, dtype=torch.uint8)
+    gbias = (torch.randn(E, 2 * I, generator=g) * 0.02).to(torch.bfloat16)
+    dbias = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    return (onl.gate_up_blocks(gub, Hp, Ip).contiguous(), onl.gate_up_scales(gus, Hp, Ip).contiguous(),
+            onl.down_blocks(dnb, Hp, Ip).contiguous(), onl.down_scales(dns, Hp, Ip).contiguous(),
+            onl.gate_up_bias(gbias, Ip, 1.0).contiguous(), onl.down_bias(dbias, Hp).contiguous())
+
+
+@pytest.mark.parametrize("E,H,I,Hp,Ip", [(2, 480, 480, 512, 512), (3, 1024, 512, 1024, 512)])
+def test_convert_in_place_equals_copy(E, H, I, Hp, Ip):
+    """The in-place rewrite gives the copy converter's packed bytes at the padded sizes, in
+    the caller's own memory, and is marked so that it is not converted twice."""
+    from vllm_neuron_amd.neuron_layout import (convert_in_place, experts_from_neuron_layout,
+                                               packed_in_place)
+
+    gw, gs, dw, ds, gb, db = _neuron_tensors(E, H, I, Hp, Ip, E * 7 + H)
+    want = experts_from_neuron_layout(gw, gs, dw, ds, Hp, Ip)
+    ptrs = [t.data_ptr() for t in (gw, gs, dw, ds)]
+    assert packed_in_place(gw, gs, dw, ds) is None
+    views = convert_in_place(gw, gs, dw, ds)
+    for v, w, p in zip(views, (want.gu_q, want.gu_s, want.dn_q, want.dn_s), ptrs):
+        assert v.data_ptr() == p and torch.equal(v, w)
+    assert gw.dtype == torch.uint16 and gw.dim() == 5  # the caller's tensors keep their type
+    again = packed_in_place(gw, gs, dw, ds)
+    assert again is not None and all(torch.equal(a, v) for a, v in zip(again, views))
+    # a second call returns the views without converting again
+    views2 = convert_in_place(gw, gs, dw, ds)
+    assert all(torch.equal(a, w) for a, w in zip(views2, (want.gu_q, want.gu_s, want.dn_q,
+                                                         want.dn_s)))
+
+
+def test_convert_in_place_reload_and_views():
+    """A reload written into the tensor (a version bump) clears the mark; views and tensors
+    that share their storage are refused."""
+    from vllm_neuron_amd.neuron_layout import (convert_in_place, experts_from_neuron_layout,
+                                               packed_in_place)
+
+    gw, gs, dw, ds, _, _ = _neuron_tensors(2, 512, 512, 512, 512, 5)
+    orig = [t.clone() for t in (gw, gs, dw, ds)]
+    want = experts_from_neuron_layout(gw, gs, dw, ds, 512, 512)
+    convert_in_place(gw, gs, dw, ds)
+    gw.copy_(orig[0])  # the caller reloads one tensor in the Trainium layout
+    assert packed_in_place(gw, gs, dw, ds) is None
+    with pytest.raises(ValueError):
+        convert_in_place(gw[:1], gs[:1], dw[:1], ds[:1])  # views
+    big = torch.zeros(2 * gw.numel(), dtype=torch.uint16)
+    shared = big[:gw.numel()].view(gw.shape)
+    with pytest.raises(ValueError):
+        convert_in_place(shared, gs, dw, ds)
+    # fresh Trainium tensors convert again to the same bytes
+    fresh = [t.clone() for t in orig]
+    views = convert_in_place(*fresh)
+    assert torch.equal(views[0], want.gu_q) and torch.equal(views[3], want.dn_s)
+
+
+def test_operators_take_in_place_experts():
+    """resolve_experts with in-place conversion on: the caller's tensors become the packed
+    experts (no copy is cached), biases as the copy path converts them; with it off the
+    copy path is unchanged."""
+    from vllm_neuron_amd.functional.moe import _cache
+    from vllm_neuron_amd.functional.moe._common import resolve_experts
+    from vllm_neuron_amd.neuron_layout import set_convert_in_place
+
+    E, Hp, Ip = 2, 512, 512
+    gw, gs, dw, ds, gb, db = _neuron_tensors(E, 480, 480, Hp, Ip, 11)
+    gb5 = gb.view(E, Ip // 4, 2, 1, 4)  # the model's 5-D bias view (model_mxfp4.py:1195-1201)
+    copy = resolve_experts(gw, gs, dw, ds, gb5, db)
+    assert copy.gu_q.data_ptr() != gw.data_ptr()
+    prev = set_convert_in_place(True)
+    try:
+        ex = resolve_experts(gw, gs, dw, ds, gb5, db)
+        assert ex.gu_q.data_ptr() == gw.data_ptr() and ex.dn_s.data_ptr() == ds.data_ptr()
+        for name in ("gu_q", "gu_s", "dn_q", "dn_s", "gu_bias", "dn_bias"):
+            assert torch.equal(getattr(ex, name), getattr(copy, name)), name
+        assert (ex.E, ex.H, ex.I) == (copy.E, copy.H, copy.I)
+        ex2 = resolve_experts(gw, gs, dw, ds, gb5, db)
+        assert ex2.gu_q.data_ptr() == gw.data_ptr() and torch.equal(ex2.gu_q, copy.gu_q)
+    finally:
+        set_convert_in_place(prev)
+        _cache.clear()

@@ -92,6 +92,11 @@ def derived(tag: str, inputs: Sequence[Optional[Tensor]], make: Callable[[], obj
     return value
 
 
+def discard(key: Tensor) -> None:
+    """Drop every value cached for ``key``'s base (its content is about to change)."""
+    _ENTRIES.pop(_base(key), None)
+
+
 def entries() -> int:
     """Number of live source tensors with cached values."""
     return len(_ENTRIES)

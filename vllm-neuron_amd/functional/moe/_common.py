@@ -9,8 +9,10 @@ from torch import Tensor
 
 from ... import _lib
 from ...enums import member_name
-from ...neuron_layout import experts_from_neuron_layout
-from ._cache import derived
+from ...neuron_layout import (convert_in_place, convert_in_place_enabled,
+                              experts_from_neuron_layout, owns_memory, packed_in_place,
+                              unshuffle_hidden_dim, untile_gate_up_bias)
+from ._cache import derived, discard
 
 
 def act_code(act) -> int:
@@ -147,7 +149,9 @@ def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
     the tiled order (any view of it, e.g. the 5-D one of :1195-1201), down bias [E, H]
     with the hidden dim shuffled) -> packed experts at the padded sizes.  The padding
     the reference's loaders add is all zeros (codes, scales, biases), so the padded rows
-    and columns add exact zeros.  Converted once per tensor version."""
+    and columns add exact zeros.  Converted once per tensor version into a cached copy, or,
+    with in-place conversion on (neuron_layout.set_convert_in_place) and tensors that own
+    their memory, rewritten in place once and used as views from then on."""
     for t, n, d in ((gu_w, "gate_up weight", 5), (gu_s, "gate_up scale", 5),
                     (dn_w, "down weight", 4), (dn_s, "down scale", 4)):
         if t is None:
@@ -177,6 +181,20 @@ def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
     for b, n in ((gu_b, "gate_up bias"), (dn_b, "down bias")):
         if b is not None and b.dtype != torch.bfloat16:
             raise NotImplementedError(f"{n} must be bfloat16")
+
+    packed = packed_in_place(gu_w, gu_s, dn_w, dn_s)
+    if packed is None and convert_in_place_enabled() and all(
+            owns_memory(t) for t in (gu_w, gu_s, dn_w, dn_s)):
+        discard(gu_w)  # a converted copy made before is stale from here on
+        packed = convert_in_place(gu_w, gu_s, dn_w, dn_s)
+    if packed is not None:  # the caller's tensors hold the packed bytes: views, no copy
+        gub = None if gu_b is None else derived(
+            "neuron_gu_bias", (gu_b,),
+            lambda: untile_gate_up_bias(gu_b.reshape(E, 2 * I_pad), I_pad).contiguous())
+        dnb = None if dn_b is None else derived(
+            "neuron_dn_bias", (dn_b,),
+            lambda: unshuffle_hidden_dim(dn_b.reshape(E, H_pad), -1).contiguous())
+        return Experts(*packed, gub, dnb, E, H_pad, I_pad)
 
     def make():
         ex = experts_from_neuron_layout(

@@ -17,6 +17,7 @@ Every step is a pure permutation of bytes (torch views, permutes and slices); th
 from __future__ import annotations
 
 import math
+import os
 from typing import Optional
 
 import torch
@@ -145,3 +146,112 @@ def experts_from_neuron_layout(gate_up_blocks: torch.Tensor, gate_up_scales: tor
         dnb = unshuffle_hidden_dim(down_bias, -1)[:, :H].contiguous()
     return MXFP4Experts.from_split(gate_b.contiguous(), gate_s.contiguous(), up_b.contiguous(),
                                    up_s.contiguous(), d.contiguous(), ds.contiguous(), gub, dnb)
+
+
+# ---------------------------------------------------------------------------------------
+# In-place conversion: no second copy of the experts in device memory.
+
+_MARK = "_mxmoe_packed_in_place"
+_in_place = os.environ.get("VLLM_NEURON_AMD_CONVERT_IN_PLACE", "0") == "1"
+
+
+def set_convert_in_place(enabled: bool) -> bool:
+    """Whether the MoE operators, handed Trainium-layout MXFP4 experts, rewrite them in
+    place (``convert_in_place``) instead of keeping a converted copy.  Off by default (the
+    caller's tensors then stay as they are); the environment variable
+    ``VLLM_NEURON_AMD_CONVERT_IN_PLACE=1`` turns it on at import.  Returns the previous
+    setting."""
+    global _in_place
+    prev, _in_place = _in_place, bool(enabled)
+    return prev
+
+
+def convert_in_place_enabled() -> bool:
+    return _in_place
+
+
+def _version(t: torch.Tensor):
+    try:
+        return t._version
+    except RuntimeError:  # inference tensors keep no version counter
+        return None
+
+
+def owns_memory(t: torch.Tensor) -> bool:
+    """Not a view, and alone in its storage: a version bump then means this tensor was
+    written."""
+    return (t._base is None and t.storage_offset() == 0 and t.is_contiguous()
+            and t.untyped_storage().nbytes() == t.numel() * t.element_size())
+
+
+def _packed_views(gu_w, gu_s, dn_w, dn_s, H_pad: int, I_pad: int):
+    """The four tensors' bytes viewed as packed experts at the padded sizes."""
+    E = gu_w.shape[0]
+
+    def flat(t):
+        return t.view(torch.uint8).reshape(-1)
+
+    return (flat(gu_w).view(E, 2 * I_pad // 16, 8 * H_pad),
+            flat(gu_s).view(E, (2 * I_pad + 63) // 64, 2 * H_pad),
+            flat(dn_w).view(E, H_pad // 16, 8 * I_pad),
+            flat(dn_s).view(E, (H_pad + 63) // 64, 2 * I_pad))
+
+
+def packed_in_place(gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
+                    down_blocks: torch.Tensor, down_scales: torch.Tensor):
+    """The packed views (gu_q, gu_s, dn_q, dn_s) of tensors that ``convert_in_place``
+    rewrote, or None: None as well when any of them was written in place since (a reload
+    in the Trainium layout bumps its version counter)."""
+    ts = (gate_up_blocks, gate_up_scales, down_blocks, down_scales)
+    marks = [getattr(t, _MARK, None) for t in ts]
+    if any(m is None or m[0] != _version(t) or m[1] != marks[0][1] for t, m in zip(ts, marks)):
+        return None
+    return _packed_views(*ts, *marks[0][1])
+
+
+def convert_in_place(gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
+                     down_blocks: torch.Tensor, down_scales: torch.Tensor):
+    """Rewrite the reference's Trainium-layout MXFP4 expert tensors (the shapes of
+    ``experts_from_neuron_layout``'s first four arguments) into this build's packed layout
+    at the padded sizes H_pad, I_pad, expert by expert, and return the packed views
+    (gu_q, gu_s, dn_q, dn_s) of the same memory.  Per expert both layouts take the same
+    bytes (gate_up I_pad H_pad data and I_pad H_pad / 16 scale bytes, down half of each,
+    the expert dim leading in both), so no second copy of the experts is kept: the
+    temporaries are one expert's.  The tensors keep their shapes and dtypes; each is marked
+    (an attribute with its version counter) so that the MoE operators take the packed views
+    from then on (``packed_in_place``).  Anything else that reads these tensors afterwards
+    sees packed bytes; a later in-place write to one of them (reloading it in the Trainium
+    layout) clears the mark.  Each tensor must own its memory (not a view, alone in its
+    storage: the reference's per-layer parameters are), so that its version counter tells
+    whether it was written."""
+    ts = (gate_up_blocks, gate_up_scales, down_blocks, down_scales)
+    done = packed_in_place(*ts)
+    if done is not None:
+        return done
+    if gate_up_blocks.dtype not in (torch.uint16, torch.int16) or gate_up_blocks.dim() != 5:
+        raise TypeError("gate_up_blocks must be the 5-D uint16 Trainium-layout tensor")
+    for t in ts:
+        if not owns_memory(t):
+            raise ValueError("in-place conversion needs tensors that own their memory "
+                             "(contiguous, not views, alone in their storage)")
+    E = gate_up_blocks.shape[0]
+    H_pad = gate_up_blocks.shape[3] * 512
+    I_pad = gate_up_scales.shape[4]
+    views = _packed_views(*ts, H_pad, I_pad) if all(
+        t.numel() * t.element_size() == n for t, n in zip(
+            ts, (E * H_pad * I_pad, E * H_pad * I_pad // 16, E * H_pad * I_pad // 2,
+                 E * H_pad * I_pad // 32))) else None
+    if views is None:
+        raise ValueError("tensor sizes do not match the Trainium layout at H_pad="
+                         f"{H_pad}, I_pad={I_pad}")
+    with torch.no_grad():
+        for e in range(E):
+            # expert e's packed bytes are materialized before they overwrite its Trainium ones
+            ex = experts_from_neuron_layout(gate_up_blocks[e:e + 1], gate_up_scales[e:e + 1],
+                                            down_blocks[e:e + 1], down_scales[e:e + 1], H_pad,
+                                            I_pad)
+            for v, p in zip(views, (ex.gu_q, ex.gu_s, ex.dn_q, ex.dn_s)):
+                v[e].copy_(p[0])
+    for t in ts:
+        setattr(t, _MARK, (_version(t), (H_pad, I_pad)))
+    return views
