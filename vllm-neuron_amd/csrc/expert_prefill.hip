@@ -845,7 +845,9 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_kernel(
 // loaded unconditionally (entries past K re-read entry 0, rows past the token's pairs
 // re-read its first row), so that each batch of loads issues together and is waited for
 // once: loads under per-entry conditions were each waited for on their own.
-template <int KM>
+// NG: column groups of 512 per pass (each lane 8 columns of a group, KM rows of each in
+// flight): 6 at top-4 covers H <= 3,072 in one pass, so a token's rows are one round trip.
+template <int KM, int NG>
 __global__ void __launch_bounds__(kCombineThreads) cte_combine_tok_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ tslot,
     const int32_t* __restrict__ tsel, const float* __restrict__ tval, int T, int H, int K,
@@ -889,7 +891,7 @@ __global__ void __launch_bounds__(kCombineThreads) cte_combine_tok_kernel(
 #pragma unroll
   for (int k = 0; k < KM; ++k) cnt += es[k] != 0x7fffffff ? 1 : 0;
   // NG column groups of 8 per lane and pass, KM rows each: all NG x KM loads in flight.
-  constexpr int NG = 16 / KM;
+  static_assert(NG * KM <= 24, "rows in flight per lane (registers)");
   typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
   for (int n = lane * 8; n < H; n += 64 * 8 * NG) {
     u16x8 b[NG][KM];
@@ -1346,12 +1348,12 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
                        w.inv, token_position_to_id, block_to_expert, n_slots, (int)block_size,
                        expert_const, (int)H, (int)E, out_f32, out);
   else if (tok_pairs && pairs->K <= 4)
-    hipLaunchKernelGGL(cte_combine_tok_kernel<4>,
+    hipLaunchKernelGGL((cte_combine_tok_kernel<4, 6>),
                        dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
                        dim3(kCombineThreads), 0, s, w.y, pairs->slot, pairs->sel, pairs->val,
                        (int)T, (int)H, pairs->K, scale_mode, out_f32, out);
   else if (tok_pairs)
-    hipLaunchKernelGGL(cte_combine_tok_kernel<8>,
+    hipLaunchKernelGGL((cte_combine_tok_kernel<8, 2>),
                        dim3((unsigned)((T + kCombineTok - 1) / kCombineTok)),
                        dim3(kCombineThreads), 0, s, w.y, pairs->slot, pairs->sel, pairs->val,
                        (int)T, (int)H, pairs->K, scale_mode, out_f32, out);
