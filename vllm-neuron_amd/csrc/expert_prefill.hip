@@ -1238,8 +1238,11 @@ int cte_run(const uint16_t* x, const float* affinities_masked, const uint8_t* gu
             void* workspace, size_t workspace_bytes, void* const* stage_events,
             const int2* order_pre, hipStream_t s, const CteTokPairs* pairs) {
   const bool bf16w = weight_fmt == MXMOE_WFMT_BF16;
-  MXMOE_REQUIRE(x && affinities_masked && gu_q && dn_q && (bf16w || (gu_s && dn_s)) &&
-                    token_position_to_id && block_to_expert && out && workspace,
+  // the affinities are read by the pre-scaling modes and the inverse-table combine only
+  const bool need_aff = !(pairs && pairs->K <= 8 && scale_mode == MXMOE_SCALE_POST);
+  MXMOE_REQUIRE(x && (affinities_masked || !need_aff) && gu_q && dn_q &&
+                    (bf16w || (gu_s && dn_s)) && token_position_to_id && block_to_expert &&
+                    out && workspace,
                 "moe_cte: null pointer");
   MXMOE_REQUIRE(T >= 1 && E >= 1 && E <= kCteMaxE && n_blocks >= 1,
                 "moe_cte: bad T/E/n_blocks (E at most %d)", kCteMaxE);

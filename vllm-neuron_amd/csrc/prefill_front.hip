@@ -222,10 +222,11 @@ __global__ void __launch_bounds__(256) pf_logits_kernel(const uint16_t* __restri
 // four waves per SIMD hide it (16-lane rows with four tokens per wave and one wave per SIMD
 // measured 11.3 against 9.4 us at 4,096 tokens and 128 experts).  Per token: the logits as
 // the router kernel forms them (partial sums 0..3 in order, plus the bias rounded to
-// bias_rnd, the sum rounded to logit_rnd), top-k and activation, the masked affinity row
-// aff_m[t] (a * padding_mask, as bw_count_kernel writes it), sel[t][k] = the k-th selected
-// expert if its affinity is nonzero, else -1, and val[t][k] its masked affinity (the value
-// aff_m[t] holds for it: the combine's weight); each nonzero affinity sets bit t % 64 of the
+// bias_rnd, the sum rounded to logit_rnd), top-k and activation, sel[t][k] = the k-th
+// selected expert if its affinity a is nonzero, else -1, and val[t][k] its masked affinity
+// a * padding_mask (the combine's weight; the value the masked affinity row that
+// bw_count_kernel reads holds for it, a row the fused flow never needs, since its scaling is
+// after the down GEMM and its combine reads these pairs); each nonzero affinity sets bit t % 64 of the
 // token's 64-token chunk mask of its expert, chunk_masks[t / 64][e] (zeroed by the logits
 // kernel; an OR commutes, so the masks are those bw_count_kernel writes).  The workgroups
 // also fill token_position_to_id with -1.  P: values per lane.
@@ -234,8 +235,7 @@ template <int P>
 __global__ void __launch_bounds__(256) pf_topk_kernel(
     const float* __restrict__ part, const void* __restrict__ bias, int bias_dt, int bias_rnd,
     int logit_rnd, int T, int E, int K, int act, int act_first, int renorm, float renorm_eps,
-    int rnd, const uint8_t* __restrict__ pmask, float* __restrict__ aff_m,
-    int32_t* __restrict__ sel, float* __restrict__ val,
+    int rnd, const uint8_t* __restrict__ pmask, int32_t* __restrict__ sel, float* __restrict__ val,
     unsigned long long* __restrict__ chunk_masks, int32_t* __restrict__ tp2id,
     int64_t n_slots) {
   const int tid = threadIdx.x, lane = tid & 63, b = blockIdx.x;
@@ -272,7 +272,6 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
   float out[8];
   topk_row_wave<P>(v, E, K, act, act_first, renorm, renorm_eps, rnd, sel_idx, out);
   const float pm = pmask ? (pmask[t] ? 1.0f : 0.0f) : 1.0f;
-  float* mrow = aff_m + (size_t)t * E;
   unsigned long long* mk = chunk_masks + (size_t)(t / kPfTok) * E;
   const unsigned long long bit = 1ull << (t % kPfTok);
 #pragma unroll
@@ -283,7 +282,6 @@ __global__ void __launch_bounds__(256) pf_topk_kernel(
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (k < K && sel_idx[k] == e) a = out[k];
-    mrow[e] = pmask ? a * pm : a;
     if (a != 0.0f) atomicOr(mk + e, bit);
   }
   if (lane < K) {
@@ -418,7 +416,7 @@ __global__ void __launch_bounds__(kOrderThreads) pf_place_kernel(
 }
 
 struct PfWs {
-  float *part, *aff_m, *val;
+  float *part, *val;
   int32_t *sel, *tslot, *tp2id, *b2e;
   unsigned long long* masks;
   int2* order;
@@ -433,7 +431,6 @@ static size_t pf_carve(void* base, size_t cap, int64_t T, int64_t H, int64_t I, 
   const int64_t nch = (T + kPfTok - 1) / kPfTok;
   const int64_t nb = blockwise_n_blocks(T, E, K, B);
   c.part = cv.take<float>(kPfParts * T * E);
-  c.aff_m = cv.take<float>(T * E);
   c.sel = cv.take<int32_t>(T * K);
   c.val = cv.take<float>(T * K);
   c.tslot = cv.take<int32_t>(T * K);
@@ -548,7 +545,7 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
 #define MXMOE_PFT(P)                                                                          \
   hipLaunchKernelGGL(pf_topk_kernel<P>, tg, dim3(256), 0, s, w.part, r.bias, r.bias_dt,       \
                      r.bias_rnd, r.logit_rnd, (int)T, (int)E, top_k, router_act, af, rn,       \
-                     renorm_eps, r.act_rnd, padding_mask, w.aff_m, w.sel, w.val, w.masks,      \
+                     renorm_eps, r.act_rnd, padding_mask, w.sel, w.val, w.masks,      \
                      w.tp2id, n_slots)
   switch (topk_per_lane((int)E)) {
     case 1: MXMOE_PFT(1); break;
@@ -572,7 +569,7 @@ extern "C" int mxmoe_moe_prefill(const uint16_t* x, const void* router_w, int ro
     cev = cte_ev;
   }
   const CteTokPairs pairs = {w.tslot, w.sel, w.val, top_k};
-  return cte_run(x, w.aff_m, gu_q, gu_s, dn_q, dn_s, weight_fmt, gu_bias, dn_bias, nullptr,
+  return cte_run(x, nullptr, gu_q, gu_s, dn_q, dn_s, weight_fmt, gu_bias, dn_bias, nullptr,
                  w.tp2id, w.b2e, n_blocks, block_size, T, H, I, E, act, clamps,
                  MXMOE_SCALE_POST, out_f32, out, w.cte, w.cte_bytes, cev, w.order, s, &pairs);
 }
