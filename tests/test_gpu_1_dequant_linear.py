@@ -58,6 +58,27 @@ def test_linear(dev, M, N, K):
     assert (d.mean() / want.abs().mean()).item() < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 5760, 2880), (1, 16, 32), (37, 48, 96),
+                                   (256, 320, 4128), (17, 4096, 2048)])
+def test_linear_few_rows_equals_tiled(dev, M, N, K):
+    """x of at most 256 rows takes the row-group kernel (one wave per 16 rows of W, K in
+    slabs through LDS); its output equals the tiled GEMM's bit for bit.  The tiled GEMM's
+    rows come from the same x padded to 257 rows (rows are independent)."""
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.functional import mxfp4_linear
+    from vllm_neuron_amd.weights import pack_mxfp4
+
+    blocks, scales = synthetic.mxfp4_tensor(31 + N, N, K)
+    x = synthetic.normal_bf16(32 + M, (M, K))
+    wq, ws = pack_mxfp4(blocks, scales)
+    wq, ws = wq.to(dev), ws.to(dev)
+    got = mxfp4_linear(x.to(dev), wq, ws).cpu()
+    xb = torch.zeros(257, K, dtype=torch.bfloat16)
+    xb[:M] = x
+    tiled = mxfp4_linear(xb.to(dev), wq, ws).cpu()[:M]
+    assert torch.equal(got.view(torch.int16), tiled.view(torch.int16))
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 16, 32), (37, 48, 96), (64, 80, 416), (300, 64, 2048),
                                    (128, 5760, 2880)])
 def test_linear_mxfp8(dev, M, N, K):
