@@ -1474,9 +1474,13 @@ extern "C" int mxmoe_moe_decode(const uint16_t* x, const void* router_w, int rou
       hipLaunchKernelGGL(front_logits_kernel<false>, fg, dim3(64 * kFrontWaves), 0, s, x, r.w,
                          d.part, (int)T, (int)H, (int)E);
     const int af = act_before_topk ? 1 : 0, rn = renorm ? 1 : 0;
-    // One token tile: one workgroup takes the top-k and routes (one launch less).  More
-    // tiles: the top-k spreads over a workgroup per tile, then the routing kernel.
-    const bool fused = T <= 16;
+    // One token tile, or up to 64 tokens over at most 64 experts: one workgroup takes the
+    // top-k and routes (one launch less).  Else the top-k spreads over a workgroup per
+    // tile, then the routing kernel.  Same box, alternating runs, us per step: 20B-shaped
+    // layer (32 experts) 24 / 32 / 48 / 64 tokens 98.7 / 96.2 / 100.3 / 107.8 -> 93.8 / 95.6 /
+    // 100.3 / 104.9; the 120B-shaped layer (128 experts) at 64 tokens 262.2 -> 263.6, so it
+    // keeps two launches there.
+    const bool fused = T <= 16 || (T <= 64 && E <= 64);
 #define MXMOE_FRONT(P)                                                                       \
   if (fused)                                                                                 \
     hipLaunchKernelGGL(front_route_kernel<P>, dim3(1), dim3(1024), 0, s, d.part, router_b,    \
