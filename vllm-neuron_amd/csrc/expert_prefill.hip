@@ -1391,149 +1391,118 @@ extern "C" int mxmoe_moe_cte(const uint16_t* x, const float* affinities_masked,
 
 // The linear for few rows of x (M <= kLinSmallM, MXFP4).  The tiled GEMM above gives such
 // an x one M-tile, so W's N / 256 N-tiles are its only workgroups (23 for N = 5,760, about
-// 40 us each, MFMA-issue bound on one wave per SIMD).  Here a workgroup is 8 waves, one row
-// group (16 rows of W) each, against a 32-row block of x (two 16-row tiles):
-// ceil(N / 128) x ceil(M / 32) workgroups (180 for 128 x 5,760, one per CU), the x blocks
-// of one block of W rows on one XCD (the dispatcher deals workgroup i to XCD i % 8), so
-// that its L2 serves those W rows to all of them.  K goes in slabs of up to kLinWChunks
-// chunks: every wave issues its row group's weight and scale loads for the whole slab at
-// once (registers), and the x block's slab goes through LDS in two halves of up to
-// kLinXChunks chunks (16-byte blocks XOR-swizzled by row), the second half's loads in
-// flight during the first half's MFMAs.  Per accumulator the arithmetic is the tiled
-// GEMM's: the same lane -> K mapping, chunks in order, steps j = 0..3 in order, lanes past
-// K with scale 0, the same bf16 conversion; so the output is the same, bit for bit.
+// 40 us each, MFMA-issue bound on one wave per SIMD).  Here a workgroup is 12 waves, one
+// row group (16 rows of W) each, against one 16-row tile of x: ceil(N / 192) x ceil(M / 16)
+// workgroups (240 for 128 x 5,760, one per CU), the x tiles of one block of W rows on one
+// XCD (the dispatcher deals workgroup i to XCD i % 8), so that its L2 serves those W rows
+// to all of them.  K goes in slabs of up to kLinSlab chunks, each one round trip: every
+// wave issues its row group's weight and scale loads for the whole slab (registers) and
+// its share of the x tile's slab as direct global -> LDS loads (no registers; 16-byte
+// blocks XOR-swizzled by row), waits for all of them, and after the barrier runs the
+// slab's MFMAs.  Per accumulator the arithmetic is the tiled GEMM's: the same lane -> K
+// mapping, chunks in order, steps j = 0..3 in order, lanes past K with scale 0, the same
+// bf16 conversion; so the output is the same, bit for bit.
 namespace mxmoe {
 
-constexpr int kLinWaves = 8;
-constexpr int kLinTiles = 2;     // 16-row x tiles per workgroup (every wave takes both)
-constexpr int kLinWChunks = 16;  // chunks per K slab: 64 + 16 registers of weights, scales
-constexpr int kLinXChunks = 8;   // chunks per LDS half: 32 rows x 8 x 256 B = 64 KiB
+constexpr int kLinWaves = 12;
+constexpr int kLinSlab = 24;  // chunks per K slab: 96 + 24 registers of weights and scales
 constexpr int kLinSmallM = 256;
-constexpr int kLinXIters = 16 * kLinTiles * 16 * kLinXChunks / (64 * kLinWaves);
-static_assert(kLinWChunks == 2 * kLinXChunks, "a K slab is two LDS halves");
-static_assert(kLinXIters * 64 * kLinWaves == 16 * kLinTiles * 16 * kLinXChunks,
-              "x blocks per thread and LDS half");
+constexpr int kLinDma = 4 * kLinSlab / kLinWaves;  // 1 KiB direct loads per wave and slab
+static_assert(kLinDma * kLinWaves == 4 * kLinSlab, "a slab's x tile: 4 KiB per chunk");
 
 __global__ void __launch_bounds__(64 * kLinWaves) linear_small_kernel(
     const uint16_t* __restrict__ x, int M, const uint8_t* __restrict__ wq,
-    const uint8_t* __restrict__ ws, int N, int K, int n_xb, uint16_t* __restrict__ y) {
-  __shared__ __attribute__((aligned(16))) uint8_t lin_lds[16 * kLinTiles * kLinXChunks * 256];
-  constexpr int XR = 16 * kLinTiles;  // x rows per workgroup
-  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, r16 = lane & 15;
+    const uint8_t* __restrict__ ws, int N, int K, int n_tiles, uint16_t* __restrict__ y) {
+  // LDS: chunk c of the slab at c * 4 KiB, row r (of 16) at r * 256 B in it, 16-byte slot s
+  // of the row holding the row's column block s ^ r
+  extern __shared__ __attribute__((aligned(16))) uint8_t lin_lds[];
+  const int lane = threadIdx.x & 63, q = lane >> 4, r16 = lane & 15;
+  const int wave = wave_id();
   const int n_rg = N / 16;
-  // workgroup i: XCD i % 8 takes the row blocks i % 8, i % 8 + 8, ..., each with its n_xb
-  // x blocks in a row; ids past the last row block exit at once (the whole workgroup)
+  // workgroup i: XCD i % 8 takes the row blocks i % 8, i % 8 + 8, ..., each with its
+  // n_tiles x tiles in a row; ids past the last row block exit at once (the whole workgroup)
   const int xcd = (int)blockIdx.x % 8, k = (int)blockIdx.x / 8;
-  const int rb = xcd + 8 * (k / n_xb);
+  const int rb = xcd + 8 * (k / n_tiles);
   if (rb * kLinWaves >= n_rg) return;
-  const int rg_raw = rb * kLinWaves + wave_id();
+  const int rg_raw = rb * kLinWaves + wave;
   const bool rg_ok = rg_raw < n_rg;
   const int rg = rg_ok ? rg_raw : n_rg - 1;  // waves past N load a real row group, store nothing
-  const int m0 = (k % n_xb) * XR;
+  const int m0 = (k % n_tiles) * 16;
   const int nc = (K + 127) / 128, nfull = K / 128, tail_q = (K % 128) / 32;
   const uint8_t* wbase = wq + (size_t)rg * ((size_t)K * 8);
   const uint8_t* sbase = ws + (size_t)(rg / 4) * ((size_t)K * 2);
   const int sshift = 8 * (rg % 4);
-  f32x4 acc[kLinTiles];
-#pragma unroll
-  for (int t = 0; t < kLinTiles; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // x chunks [h0, h0 + nh) of the block into registers: block id -> (row id / (16 nh),
-  // column block); rows past M re-read row M - 1, blocks past K re-read column 0 (their
-  // weights are zero), ids past the half re-read its last block (stored again, same value:
-  // no branch, so the compiler keeps every load ahead of the first store).
-  const char* x8 = reinterpret_cast<const char*>(x);  // M K < 2^31 elements: 32-bit offsets
-  auto xload = [&](u32x4 (&xv)[kLinXIters], int h0, int nh) {
-#pragma unroll
-    for (int u = 0; u < kLinXIters; ++u) {
-      const int id = min(tid + 64 * kLinWaves * u, XR * 16 * nh - 1);
-      const int row = id / (16 * nh), b = id - row * (16 * nh);
-      const int col = (h0 + (b >> 4)) * 128 + 8 * (b & 15);
-      const int m = min(m0 + row, M - 1);
-      xv[u] = *reinterpret_cast<const u32x4*>(
-          x8 + 2u * ((uint32_t)m * (uint32_t)K + (uint32_t)(col < K ? col : 0)));
-    }
-  };
-  auto xstore = [&](const u32x4 (&xv)[kLinXIters], int nh) {
-#pragma unroll
-    for (int u = 0; u < kLinXIters; ++u) {
-      const int id = min(tid + 64 * kLinWaves * u, XR * 16 * nh - 1);
-      const int row = id / (16 * nh), b = id - row * (16 * nh);
-      *reinterpret_cast<u32x4*>(lin_lds + row * (kLinXChunks * 256) + (b >> 4) * 256 +
-                                (((b & 15) ^ (row & 15)) << 4)) = xv[u];
-    }
-  };
-  for (int c0 = 0; c0 < nc; c0 += kLinWChunks) {
-    const int ns = min(kLinWChunks, nc - c0);
-    const int na = min(kLinXChunks, ns), nb = ns - na;  // the two halves' chunks
-    // The first x half's loads, then the slab's weights and scales, all issued before any
-    // wait; the scheduling barriers keep that order (left alone, the compiler interleaved
-    // the x loads with their LDS stores, one round trip each).  Chunks past the slab re-read
-    // its last one; lanes past K read lane 0's bytes, which the zero scale cancels.
-    u32x4 xa[kLinXIters];
-    xload(xa, c0, na);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 wv[kLinWChunks];
-    uint32_t sv[kLinWChunks];
-#pragma unroll
-    for (int i = 0; i < kLinWChunks; ++i) {
+  // this lane's x row in direct load i of a chunk (rows 4i .. 4i + 3, 16 lanes each) and
+  // its source column block (slot lane % 16 of row r holds block (lane % 16) ^ r)
+  const int drow = lane >> 4;  // + 4 * (load index % 4)
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nc; c0 += kLinSlab) {
+    const int ns = min(kLinSlab, nc - c0);
+    if (c0 > 0) __syncthreads();  // the last slab's LDS is read before it is refilled
+    // The x tile's slab: wave w issues loads d = w, w + 12, ... < 4 ns, load d = (chunk
+    // d / 4, rows 4 (d % 4) ..), 1 KiB to LDS offset d * 1 KiB; loads u < kLinDma / 2 hold
+    // chunks 0 .. 11 of the slab, the others chunks 12 .. 23.
+    auto xdma = [&](int u) {
+      const int d = wave + kLinWaves * u;
+      if (d < 4 * ns) {
+        const int row = 4 * (d & 3) + drow;
+        const int col = (c0 + (d >> 2)) * 128 + 8 * (r16 ^ row);
+        const int m = min(m0 + row, M - 1);
+        const uint32_t off = 2u * ((uint32_t)m * (uint32_t)K + (uint32_t)(col < K ? col : 0));
+        const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
+            const __attribute__((address_space(3))) uint8_t*)(lin_lds + d * 1024));
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+                     "s"(x)
+                     : "memory", "m0");
+      }
+    };
+    // The slab's weights and scales (chunks past the slab re-read its last one; lanes past
+    // K read lane 0's bytes, which the zero scale cancels).
+    u32x4 wv[kLinSlab];
+    uint32_t sv[kLinSlab];
+    auto wload = [&](int i) {
       const int c = c0 + min(i, ns - 1);
       const uint32_t lo = (c < nfull || q < tail_q) ? (uint32_t)lane : 0u;
       wv[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)c * 1024 + lo * 16u);
       sv[i] = *reinterpret_cast<const uint32_t*>(sbase + (size_t)c * 256 + lo * 4u);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // Chunks I0 + ii, ii in [II0, II1) and < n, of the slab against the LDS half that
-    // holds chunk I0 first.
-    auto compute = [&](auto i0_c, auto ii0_c, auto ii1_c, int n) {
-      constexpr int I0 = decltype(i0_c)::value, II0 = decltype(ii0_c)::value,
-                    II1 = decltype(ii1_c)::value;
+    };
+    // Issue order: the first half's x and weights, the second half's x, then its weights
+    // (2 x 12 loads, always issued); waiting until at most those 24 are outstanding leaves
+    // every x block landed (the direct loads are not counted by the compiler), and the
+    // first half's MFMAs run while the second half's weights arrive (the compiler waits
+    // for each weight register it counts before its first use).
 #pragma unroll
-      for (int ii = II0; ii < II1; ++ii) {
-        if (ii < n) {
-          const int i = I0 + ii, c = c0 + i;
-          const bool kok = c < nfull || q < tail_q;
-          const float sc = kok ? e8m0_to_f32((sv[i] >> sshift) & 0xffu) : 0.0f;
+    for (int u = 0; u < kLinDma / 2; ++u) xdma(u);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const bf16x8 a = dequant8(wv[i][j], sc);
+    for (int i = 0; i < kLinSlab / 2; ++i) wload(i);
 #pragma unroll
-            for (int t = 0; t < kLinTiles; ++t) {
-              const u32x4 xf = *reinterpret_cast<const u32x4*>(
-                  lin_lds + (16 * t + r16) * (kLinXChunks * 256) + ii * 256 +
-                  (((4 * q + j) ^ r16) << 4));
-              acc[t] = mfma16(a, as_bf16x8(xf), acc[t]);
-            }
-          }
+    for (int u = kLinDma / 2; u < kLinDma; ++u) xdma(u);
+#pragma unroll
+    for (int i = kLinSlab / 2; i < kLinSlab; ++i) wload(i);
+    static_assert(kLinSlab == 24 && kLinDma == 8, "the wait below counts 2 x 12 loads");
+    asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    __syncthreads();
+    const uint8_t* xr = lin_lds + r16 * 256;
+#pragma unroll
+    for (int i = 0; i < kLinSlab; ++i) {
+      if (i < ns) {
+        const int c = c0 + i;
+        const bool kok = c < nfull || q < tail_q;
+        const float sc = kok ? e8m0_to_f32((sv[i] >> sshift) & 0xffu) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4 xf =
+              *reinterpret_cast<const u32x4*>(xr + i * 4096 + (((4 * q + j) ^ r16) << 4));
+          acc = mfma16(dequant8(wv[i][j], sc), as_bf16x8(xf), acc);
         }
       }
-    };
-    xstore(xa, na);
-    __syncthreads();
-    using C0 = std::integral_constant<int, 0>;
-    using CH = std::integral_constant<int, kLinXChunks / 2>;
-    using CX = std::integral_constant<int, kLinXChunks>;
-    compute(C0(), C0(), CH(), na);
-    // The second half's loads, in flight during the rest of the first half's MFMAs (issued
-    // here, where the first chunks' weight registers are free again).
-    u32x4 xb[kLinXIters];
-    if (nb > 0) xload(xb, c0 + na, nb);
-    compute(C0(), CH(), CX(), na);
-    __syncthreads();  // the first half is read before the second overwrites it
-    if (nb > 0) {
-      xstore(xb, nb);
-      __syncthreads();
-      compute(CX(), C0(), CX(), nb);
-      __syncthreads();
     }
   }
-  // Lane (q, r16) of tile t: W rows 16 rg + 4q .. + 3 of x row m0 + 16 t + r16.
-#pragma unroll
-  for (int t = 0; t < kLinTiles; ++t) {
-    const int m = m0 + 16 * t + r16;
-    if (rg_ok && m < M)
-      *reinterpret_cast<u32x2*>(y + (size_t)m * N + 16 * rg + 4 * q) =
-          u32x2{pack_bf16x2(acc[t][0], acc[t][1]), pack_bf16x2(acc[t][2], acc[t][3])};
-  }
+  // Lane (q, r16): W rows 16 rg + 4q .. + 3 of x row m0 + r16.
+  const int m = m0 + r16;
+  if (rg_ok && m < M)
+    *reinterpret_cast<u32x2*>(y + (size_t)m * N + 16 * rg + 4 * q) =
+        u32x2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
 }
 
 }  // namespace mxmoe
@@ -1549,11 +1518,15 @@ extern "C" int mxmoe_linear(const uint16_t* x, int64_t M, const uint8_t* wq, con
                 (long long)K);
   if (M == 0) return MXMOE_OK;
   if (weight_fmt == MXMOE_WFMT_MXFP4 && M <= kLinSmallM) {
+    MXMOE_REQUIRE(M * K * 2 < ((int64_t)1 << 32), "linear: x of %lld x %lld too large",
+                  (long long)M, (long long)K);
+    const int nc = (int)((K + 127) / 128);
+    const size_t lds = (size_t)std::min(kLinSlab, nc) * 4096;
     const int n_rb = (int)((N / 16 + kLinWaves - 1) / kLinWaves);
-    const int n_xb = (int)((M + 16 * kLinTiles - 1) / (16 * kLinTiles));
-    hipLaunchKernelGGL(linear_small_kernel, dim3((unsigned)(8 * ((n_rb + 7) / 8) * n_xb)),
-                       dim3(64 * kLinWaves), 0, as_stream(stream), x, (int)M, wq, ws, (int)N,
-                       (int)K, n_xb, y);
+    const int n_tiles = (int)((M + 15) / 16);
+    hipLaunchKernelGGL(linear_small_kernel, dim3((unsigned)(8 * ((n_rb + 7) / 8) * n_tiles)),
+                       dim3(64 * kLinWaves), lds, as_stream(stream), x, (int)M, wq, ws, (int)N,
+                       (int)K, n_tiles, y);
     return check_launch("linear");
   }
   PrefillArgs a = {};
