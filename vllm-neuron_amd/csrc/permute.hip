@@ -93,6 +93,88 @@ __global__ void __launch_bounds__(kBwThreads) bw_scatter_kernel(
   });
 }
 
+// Passes 2 and 3 in one launch for mappings whose chunk masks are few (every workgroup
+// reads all of them): one workgroup of 1024 threads per chunk c, and one more (c =
+// n_chunks) for the block tables.  Each reads every chunk mask and forms the per-expert
+// totals (integer sums in LDS, so the atomics' order is free) and scans the experts' block
+// counts into the first slot of each run, expert_pos[e], as bw_scan_body does.  A chunk's
+// workgroup also sums pre[e], the expert's tokens in earlier chunks, keeps its own chunk's
+// masks in LDS and writes its pairs: thread e walks the set bits of its expert's mask, the
+// token of the r-th bit at slot expert_pos[e] + pre[e] + r, bw_scatter_kernel's slot.  The
+// last workgroup writes block_to_expert, conditions and expert_counts as bw_scan_body.
+constexpr int kPlaceMaxMasks = 32768;  // 256 KB of masks per workgroup at most
+__global__ void __launch_bounds__(1024) bw_place_kernel(
+    const unsigned long long* __restrict__ chunk_masks, int n_chunks, int E, int B, int N,
+    int32_t* __restrict__ tp2id, int64_t n_slots, int32_t* __restrict__ block_to_expert,
+    int32_t* __restrict__ conditions, int32_t* __restrict__ expert_counts) {
+  __shared__ int tot[kMaxE], pre[kMaxE], cum[kMaxE], wsum[16];
+  __shared__ unsigned long long own[kMaxE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
+  const bool place = c < n_chunks;
+  for (int e = tid; e < E; e += 1024) tot[e] = pre[e] = 0;
+  __syncthreads();
+  const int nm = n_chunks * E;
+  for (int i0 = 0; i0 < nm; i0 += 8 * 1024) {
+    unsigned long long m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 1024 + tid;
+      m[u] = i < nm ? chunk_masks[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 1024 + tid;
+      const int n = __popcll(m[u]);
+      if (place && i / E == c) own[i % E] = m[u];
+      if (n) {
+        const int e = i % E;
+        atomicAdd(&tot[e], n);
+        if (i / E < c) atomicAdd(&pre[e], n);
+      }
+    }
+  }
+  __syncthreads();
+  // Inclusive scan of the block counts over experts: wave scan, then across waves.
+  const int e = tid;
+  const int nb = e < E ? (tot[e] + B - 1) / B : 0;
+  int v = nb;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(v, off);
+    if (lane >= off) v += o;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) v += wsum[w];
+  if (e < E) cum[e] = v;
+  __syncthreads();
+  if (place) {
+    if (e < E) {
+      unsigned long long m = own[e];
+      int64_t pos = (int64_t)(v - nb) * B + pre[e];
+      while (m) {
+        const int bit = __ffsll((long long)m) - 1;
+        m &= m - 1;
+        if (pos < n_slots) tp2id[pos] = c * kChunkTok + bit;
+        ++pos;
+      }
+    }
+    return;
+  }
+  if (e < E && expert_counts) expert_counts[e] = tot[e];
+  const int used = cum[E - 1];
+  for (int n = tid; n < N; n += 1024) {
+    int lo = 0, hi = E - 1;  // #{e < E - 1 : n >= cum[e]} (cum is non-decreasing)
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (cum[mid] <= n) lo = mid + 1;
+      else hi = mid;
+    }
+    block_to_expert[n] = lo;
+    if (conditions) conditions[n] = n < used ? 1 : 0;
+  }
+}
+
 }  // namespace mxmoe
 
 using namespace mxmoe;
@@ -135,6 +217,12 @@ extern "C" int mxmoe_blockwise_mapping(const float* affinities, const uint8_t* p
   hipLaunchKernelGGL(bw_count_kernel, dim3((unsigned)nch), dim3(kBwThreads), lds, s, affinities,
                      padding_mask, (int)T, (int)E, (int)nch, affinities_masked, counts,
                      chunk_masks, token_position_to_id, n_slots);
+  if (nch * E <= kPlaceMaxMasks) {
+    hipLaunchKernelGGL(bw_place_kernel, dim3((unsigned)nch + 1), dim3(1024), 0, s, chunk_masks,
+                       (int)nch, (int)E, (int)block_size, (int)n_blocks, token_position_to_id,
+                       n_slots, block_to_expert, conditions, expert_counts);
+    return check_launch("blockwise_mapping");
+  }
   hipLaunchKernelGGL(bw_scan_kernel, dim3(1), dim3(1024), 0, s, counts, (int)nch, (int)E,
                      (int)block_size, (int)n_blocks, expert_pos, block_to_expert, conditions,
                      expert_counts);
