@@ -221,13 +221,14 @@ def test_derived_cache_releases_freed_sources():
     assert _cache.entries() == 0
 
 
-def test_moe_cte_no_scale_raises():
+def test_moe_cte_no_scale_is_accepted():
+    """NO_SCALE passes the mode check (it runs on the GPU: here the CPU tensors stop it)."""
     import torch
 
     from vllm_neuron_amd import functional as NF
 
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError, match="NO_SCALE"):
+    with pytest.raises(RuntimeError, match="GPU tensors"):
         NF.moe_cte(x, torch.zeros(8, 1), torch.zeros(2, 8, 512, dtype=torch.uint8),
                    torch.zeros(2, 4, 256, dtype=torch.uint8), torch.zeros(256, dtype=torch.int32),
                    torch.zeros(1, dtype=torch.int32), 256,

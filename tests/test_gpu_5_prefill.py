@@ -244,6 +244,51 @@ def test_moe_cte_prescale_modes(dev, mode, biases):
     check_close(got.float(), want.float(), None, f"moe_cte {mode} biases={biases}")
 
 
+@pytest.mark.parametrize("biases", [True, False])
+def test_moe_cte_no_scale(dev, biases):
+    """NO_SCALE against the oracle's dense torch flow: every expert's output for every token
+    added unscaled in bf16 (moe_cte.py:518-579); the caller's (routed) mapping is not used."""
+    from vllm_neuron_amd import functional as NF
+    from vllm_neuron_amd import synthetic
+    from vllm_neuron_amd.weights import MXFP4Experts
+
+    from oracle import moe_cte as oc
+    from oracle.layer import RefLayer
+
+    shape = synthetic.MoEShape("mini", 8, 2, 256, 512, biases=biases)
+    lt = synthetic.layer_tensors(shape, 38, exp_range=(118, 122))
+    ref = RefLayer(lt)
+    w = MXFP4Experts.from_checkpoint(lt.gate_up_blocks, lt.gate_up_scales, lt.down_blocks,
+                                     lt.down_scales, lt.gate_up_bias, lt.down_bias).to(dev)
+    T = 150
+    x = synthetic.tokens(38, T, ref.H)
+    aff, _ = ref.route(x)
+    am_g, tp, b2e, cond = NF.build_blockwise_mapping(aff.to(dev), 8, 2, 256)
+    got = NF.moe_cte(x.to(dev), am_g, w.gu_q, w.dn_q, tp, b2e, 256, conditions=cond,
+                     gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                     gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                     activation_function="Swish", expert_affinities_scaling_mode="NO_SCALE",
+                     gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                     up_clamp_lower_limit=-6.0).cpu()
+    gu, gb, db = ref._cte_args()
+    want = oc.torch_moe_impl(x, aff.reshape(-1, 1), gu, ref.down, gb, db,
+                             gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                             up_clamp_lower_limit=-6.0, activation_function="Swish",
+                             expert_affinities_scaling_mode="NO_SCALE")
+    assert got.dtype == torch.bfloat16 and want.dtype == torch.bfloat16
+    check_close(got.float(), want.float(), None, f"moe_cte NO_SCALE biases={biases}")
+    # the same output whatever the routing: an empty mapping gives it too
+    zero = torch.zeros_like(aff)
+    am0, tp0, b2e0, _ = NF.build_blockwise_mapping(zero.to(dev), 8, 2, 256)
+    got0 = NF.moe_cte(x.to(dev), am0, w.gu_q, w.dn_q, tp0, b2e0, 256,
+                      gate_and_up_proj_bias=w.gu_bias, down_proj_bias=w.dn_bias,
+                      gate_up_proj_scale=w.gu_s, down_proj_scale=w.dn_s,
+                      activation_function="Swish", expert_affinities_scaling_mode="NO_SCALE",
+                      gate_clamp_upper_limit=7.0, up_clamp_upper_limit=8.0,
+                      up_clamp_lower_limit=-6.0).cpu()
+    assert torch.equal(got0.view(torch.int16), got.view(torch.int16))
+
+
 def test_moe_cte_out_of_range_expert_block_is_empty(dev):
     """A block_to_expert entry outside [0, E) (the reference would raise IndexError on its
     weights) computes nothing: its slots add no term, every other block is unchanged."""

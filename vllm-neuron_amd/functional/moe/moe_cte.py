@@ -29,7 +29,12 @@ expert_affinities_scaling_mode (moe_cte.py:465-495, 518-579):
     PRE_SCALE_DELAYED, and under PRE_SCALE y_e(0) = down(act(clamp(b_gate)) *
     clamp(b_up)) + b_down, computed once per weight version by the same kernels.
   * NO_SCALE: the torch flow adds every expert's full output for every token, routed or
-    not, which a routed kernel does not compute; it raises NotImplementedError.  Trainium tuning arguments (n_block_per_iter,
+    not, unscaled (its bf16 running sum over all E experts, as for PRE_SCALE_DELAYED with
+    every affinity 1).  It runs as exactly that: a mapping that routes every token to every
+    expert (T E slots: E times the routed work, the caller's mapping unused) and the
+    PRE_SCALE_DELAYED kernels on affinities of 1, whose multiply is then exact.
+
+Trainium tuning arguments (n_block_per_iter,
 block_sharding_strategy, n_static_blocks, n_dynamic_blocks, checkpoint_activation,
 skip_weight, ...) are accepted and have no effect; ``conditions`` is not needed
 because empty blocks are detected from token_position_to_id.
@@ -81,7 +86,7 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
         raise NotImplementedError("output_dtype must be bfloat16 or float32")
     if member_name(quantization_type) == "STATIC_MX":
         raise NotImplementedError("STATIC_MX (FP8 weights) has no MI355X kernel")
-    mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=False, allow_pre=True)
+    mode = scale_code(expert_affinities_scaling_mode, allow_no_scale=True, allow_pre=True)
     if gate_up_activations_T is not None or down_activations is not None:
         raise NotImplementedError("activation checkpoint buffers are not supported")
     bf16w = is_bf16_weights(gate_up_proj_weight)
@@ -123,6 +128,8 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
                   up_clamp_upper_limit)
     act = act_code(activation_function)
     const = None
+    if mode == _lib.SCALE_NO:
+        return _no_scale(x, ex, T, block_size, act, clamp_vals, output_dtype, stage_events)
     if mode == _lib.SCALE_PRE_DELAYED:
         const = ex.dn_bias
     elif mode == _lib.SCALE_PRE and ex.gu_bias is not None:
@@ -130,6 +137,22 @@ def moe_cte(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up_pro
     out = torch.empty(T, H, dtype=output_dtype, device=dev)
     _cte_call(x, aff, ex, const, tp2id, b2e, n_blocks, block_size, T, act, clamp_vals, mode,
               out, stage_events)
+    return out
+
+
+def _no_scale(x, ex, T, block_size, act, clamp_vals, output_dtype, stage_events):
+    """NO_SCALE (moe_cte.py:518-579 with no affinity applied): every expert on every token,
+    the outputs added unscaled in expert order in bf16; the PRE_SCALE_DELAYED path over a
+    mapping of all T E (token, expert) pairs with affinity 1."""
+    from .moe_blockwise import build_blockwise_mapping
+
+    E, H = ex.E, ex.H
+    ones = torch.ones(T, E, dtype=torch.float32, device=x.device)
+    aff_m, tp2id, b2e, _ = build_blockwise_mapping(ones, E, E, block_size)
+    out = torch.empty(T, H, dtype=output_dtype, device=x.device)
+    _cte_call(x, aff_m.reshape(-1), ex, ex.dn_bias, tp2id.reshape(-1), b2e.reshape(-1),
+              b2e.numel(), block_size, T, act, clamp_vals, _lib.SCALE_PRE_DELAYED, out,
+              stage_events)
     return out
 
 
