@@ -183,7 +183,9 @@ def _from_neuron_layout(gu_w, gu_s, dn_w, dn_s, gu_b, dn_b) -> Experts:
             raise NotImplementedError(f"{n} must be bfloat16")
 
     packed = packed_in_place(gu_w, gu_s, dn_w, dn_s)
-    if packed is None and convert_in_place_enabled() and all(
+    # not while a HIP graph is being captured: its replays would rewrite the bytes again
+    if packed is None and convert_in_place_enabled() and not (
+            gu_w.is_cuda and torch.cuda.is_current_stream_capturing()) and all(
             owns_memory(t) for t in (gu_w, gu_s, dn_w, dn_s)):
         discard(gu_w)  # a converted copy made before is stale from here on
         packed = convert_in_place(gu_w, gu_s, dn_w, dn_s)
