@@ -230,6 +230,9 @@ def convert_in_place(gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
         return done
     if gate_up_blocks.dtype not in (torch.uint16, torch.int16) or gate_up_blocks.dim() != 5:
         raise TypeError("gate_up_blocks must be the 5-D uint16 Trainium-layout tensor")
+    if gate_up_blocks.is_cuda and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("convert_in_place under HIP graph capture: every replay would "
+                           "rewrite the bytes again; convert before capturing")
     for t in ts:
         if not owns_memory(t):
             raise ValueError("in-place conversion needs tensors that own their memory "
