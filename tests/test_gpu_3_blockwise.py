@@ -30,6 +30,9 @@ CASES = [
     # the largest expert count the kernels take (1,024), and a large one that is not a
     # multiple of 4 (affinity rows read one element at a time)
     (96, 1024, 8, 128, None), (130, 1001, 8, 256, 1.0),
+    # over 32K chunk masks (65 chunks x 512 experts): the scan and scatter kernels instead
+    # of the one placement kernel
+    (4160, 512, 4, 256, None),
 ]
 
 
@@ -46,12 +49,13 @@ def test_blockwise_bit_exact(dev, T, E, K, B, zipf):
     assert torch.equal(c_g.cpu(), c_r)
 
 
-def test_blockwise_padding_mask(dev):
+@pytest.mark.parametrize("T,E", [(777, 32), (4160, 512)])
+def test_blockwise_padding_mask(dev, T, E):
     from vllm_neuron_amd import functional as NF
 
-    T, E, K, B = 777, 32, 4, 256
+    K, B = 4, 256
     aff = _aff(T, E, K, 5)
-    pm = torch.arange(T) <= 500
+    pm = torch.arange(T) <= 2 * T // 3
     r = ob.build_blockwise_mapping(aff, E, K, B, padding_mask=pm)
     g = NF.build_blockwise_mapping(aff.to(dev), E, K, B, padding_mask=pm.to(dev))
     for a, b in zip(g, r):
