@@ -19,10 +19,10 @@ reference's own CPU implementation of the MXFP4 MoE path (vllm-neuron, CPU mode)
     (vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:243-885)       -> oracle.neuron_layout
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or, for the
-baseline, as the timed CPU path).  The product package never imports it; its
-functional API raises when the HIP extension is missing instead of falling
-back to anything here.
+``bench.py`` may import this package, and only as the reference the GPU results
+are compared with (or, for the baseline, as the timed CPU path).  The product
+package never imports it; its functional API raises when the HIP extension is
+missing instead of falling back to anything here.
 
 Pinning (what each function is checked against, besides the reference text it
 follows) is listed in each module's docstring; the tests under ``tests/``

@@ -1,6 +1,6 @@
 """Restatement of the reference's load-time MXFP4 transform into its Trainium kernel
-layout, for one tensor-parallel rank (TEST INFRASTRUCTURE: the checker of the
-product's converter vllm_neuron_amd.neuron_layout, which inverts it).
+layout, for one tensor-parallel rank (TEST INFRASTRUCTURE: what the tests check the
+product's converter vllm_neuron_amd.neuron_layout, which inverts it, against).
 
 Follows vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:
   gate_up blocks  mxfp4_gate_up_blocks_loader :243-311, _pack_fp4_x4_uint16 :567-587,

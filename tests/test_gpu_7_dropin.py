@@ -1,4 +1,4 @@
-"""The reference's own MXFP4 callers, run unchanged against this build's operators.
+"""The reference's own MXFP4 callers, run unchanged against this package's operators.
 
 * GptOssExperts._run_moe_block_tkg (model_mxfp4.py:1158-1214) and the prefill chain of
   forward_prefill (:1333-1436), with their argument lists as written: tensors in the

@@ -10,7 +10,7 @@ E = 1, i.e. the grouped gate_up GEMM with fused dequant, bias, clamps and activa
 the down GEMM with bias, with the torch flow's bf16 result of every op; the combine
 multiplies by 1.0, which leaves the bf16 result unchanged.
 
-Weights are this build's packed single-matrix layout (``weights.pack_mxfp4`` /
+Weights are this package's packed single-matrix layout (``weights.pack_mxfp4`` /
 ``weights.pack_mxfp8`` of the [out_features, in_features] matrix, i.e. the transpose of
 the reference's ``x @ w`` operand): gate_w and up_w [I/16, 8H] (MXFP4) or [I/16, 16H]
 (MXFP8) uint8 with scales [ceil(I/64), 2H]; down_w [H/16, 8I] or [H/16, 16I] with scales

@@ -1,4 +1,4 @@
-"""Converter from vllm-neuron's Trainium MXFP4 kernel layout to this build's packed layout.
+"""Converter from vllm-neuron's Trainium MXFP4 kernel layout to this package's packed layout.
 
 The reference prepares its MoE weights at load time into a layout tiled for its
 Trainium kernels (vllm_neuron/model/gpt_oss/weight_loaders_mxfp4.py:243-885): gate/up
@@ -212,7 +212,7 @@ def packed_in_place(gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
 def convert_in_place(gate_up_blocks: torch.Tensor, gate_up_scales: torch.Tensor,
                      down_blocks: torch.Tensor, down_scales: torch.Tensor):
     """Rewrite the reference's Trainium-layout MXFP4 expert tensors (the shapes of
-    ``experts_from_neuron_layout``'s first four arguments) into this build's packed layout
+    ``experts_from_neuron_layout``'s first four arguments) into this package's packed layout
     at the padded sizes H_pad, I_pad, expert by expert, and return the packed views
     (gu_q, gu_s, dn_q, dn_s) of the same memory.  Per expert both layouts take the same
     bytes (gate_up I_pad H_pad data and I_pad H_pad / 16 scale bytes, down half of each,
