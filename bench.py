@@ -565,7 +565,7 @@ def time_linear(dev, gen, settle_s, n_w=64, calls=256):
     nbytes = N * K // 2 + N * K // 32 + M * K * 2 + M * N * 2
     flops = 2 * M * N * K
     t_min = max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (MXFP4_PEAK_TFLOPS * 1e12))
-    return {"workload": "MXFP4 linear W 5760x2880, x 128x2880 (config 0)", "us_per_call": us,
+    return {"workload": "MXFP4 linear W 5760x2880, x 128x2880", "us_per_call": us,
             "tokens_per_s": M / (us * 1e-6), "algorithmic_bytes": nbytes,
             "algorithmic_flops": flops, "GBps": nbytes / (us * 1e-6) / 1e9,
             "TFLOPs": flops / (us * 1e-6) / 1e12, "binding_roofline": "hbm",
